@@ -1,0 +1,546 @@
+#include "runtime.h"
+
+#include <algorithm>
+#include <chrono>
+#include <cstdlib>
+#include <cstring>
+#include <stdexcept>
+
+namespace ckl::rt {
+
+void check(hipError_t status, const char *what) {
+  if (status != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(status));
+}
+
+int deviceCount() {
+  int count = 0;
+  if (hipGetDeviceCount(&count) != hipSuccess) return 0;
+  return count;
+}
+
+BranchPolicy branchPolicy() {
+  const char *value = std::getenv("CKL_GRAPH_BRANCHES");
+  return value && std::strcmp(value, "1") == 0 ? BranchPolicy::Branches : BranchPolicy::Grouped;
+}
+
+// ====================================================================== device and buffers
+static std::atomic<uint64_t> nextDeviceId{0};
+
+Device::Device(int ordinal_) : ordinal(ordinal_), id(nextDeviceId++) {
+  int count = deviceCount();
+  if (ordinal < 0 || ordinal >= count) throw std::invalid_argument("HIP device ordinal is not available");
+  makeCurrent();
+  hipDeviceProp_t props;
+  check(hipGetDeviceProperties(&props, ordinal), "hipGetDeviceProperties");
+  name = std::string(props.name[0] ? props.name : "AMD GPU") + " (" + props.gcnArchName + ")";
+}
+
+Device::~Device() {
+  std::lock_guard<std::mutex> lock(moduleMutex);
+  for (auto &[_, module] : modules) hipModuleUnload(module);
+}
+
+void Device::makeCurrent() const { check(hipSetDevice(ordinal), "hipSetDevice"); }
+
+hipModule_t Device::load(const std::string &identity, const void *image, size_t bytes) {
+  std::lock_guard<std::mutex> lock(moduleMutex);
+  auto found = modules.find(identity);
+  if (found != modules.end()) return found->second;
+  if (!image || !bytes) throw std::invalid_argument("cannot load an empty code object");
+  makeCurrent();
+  hipModule_t module = nullptr;
+  check(hipModuleLoadData(&module, image), "hipModuleLoadData");
+  modules[identity] = module;
+  return module;
+}
+
+void Buffer::copyFromHost(const void *data, uint64_t size) const {
+  if (size != bytes) throw std::invalid_argument("host buffer byte count does not match device storage");
+  device->makeCurrent();
+  check(hipMemcpy(reinterpret_cast<void *>(address()), data, size, hipMemcpyHostToDevice), "hipMemcpy(H2D)");
+  check(hipDeviceSynchronize(), "hipDeviceSynchronize");
+}
+
+void Buffer::copyToHost(void *data, uint64_t size) const {
+  if (size != bytes) throw std::invalid_argument("destination must match device storage byte count");
+  device->makeCurrent();
+  check(hipDeviceSynchronize(), "hipDeviceSynchronize");
+  check(hipMemcpy(data, reinterpret_cast<void *>(address()), size, hipMemcpyDeviceToHost), "hipMemcpy(D2H)");
+}
+
+std::shared_ptr<Buffer> allocateBuffer(std::shared_ptr<Device> device, uint64_t bytes) {
+  if (!bytes) throw std::invalid_argument("HIP allocation size must be nonzero");
+  device->makeCurrent();
+  void *pointer = nullptr;
+  check(hipMalloc(&pointer, bytes), "hipMalloc");
+  auto buffer = std::make_shared<Buffer>();
+  std::shared_ptr<Device> owner = device;
+  buffer->storage = std::shared_ptr<void>(pointer, [owner](void *p) {
+    owner->makeCurrent();
+    hipFree(p);
+  });
+  buffer->device = std::move(device);
+  buffer->base = reinterpret_cast<uint64_t>(pointer);
+  buffer->bytes = bytes;
+  return buffer;
+}
+
+std::shared_ptr<Buffer> importBuffer(std::shared_ptr<Device> device, uint64_t address, uint64_t bytes) {
+  if (!address || !bytes) throw std::invalid_argument("imported HIP buffer requires an address and size");
+  auto buffer = std::make_shared<Buffer>();
+  buffer->device = std::move(device);
+  buffer->base = address;
+  buffer->bytes = bytes;
+  return buffer;
+}
+
+std::shared_ptr<Buffer> sliceBuffer(const std::shared_ptr<Buffer> &parent, uint64_t offset, uint64_t bytes) {
+  if (!bytes || offset > parent->bytes || bytes > parent->bytes - offset)
+    throw std::out_of_range("HIP buffer slice exceeds its parent view");
+  auto buffer = std::make_shared<Buffer>(*parent);
+  buffer->offset = parent->offset + offset;
+  buffer->bytes = bytes;
+  return buffer;
+}
+
+// ====================================================================== plans
+size_t Plan::addKernel(Launch launch, std::vector<size_t> deps) {
+  if (!launch.function) throw std::invalid_argument("kernel plan node requires a resolved function");
+  for (unsigned d : launch.grid) if (!d) throw std::invalid_argument("kernel plan node requires positive launch dimensions");
+  for (unsigned d : launch.block) if (!d) throw std::invalid_argument("kernel plan node requires positive launch dimensions");
+  size_t id = nodes.size();
+  for (size_t d : deps)
+    if (d >= id) throw std::invalid_argument("kernel dependencies must reference earlier plan nodes");
+  nodes.push_back({std::move(launch), std::move(deps)});
+  return id;
+}
+
+// ExecutionPlan::repeat semantics (lib/Core/ExecutionPlan.cpp:87-117).
+Plan Plan::repeat(size_t iterations) const {
+  if (!iterations) throw std::invalid_argument("HIP plan repeat count must be nonzero");
+  if (nodes.empty()) throw std::invalid_argument("cannot repeat an empty HIP plan");
+  std::vector<bool> hasSuccessor(nodes.size(), false);
+  for (const PlanNode &n : nodes) for (size_t d : n.dependencies) hasSuccessor[d] = true;
+  std::vector<size_t> leaves;
+  for (size_t k = 0; k < nodes.size(); ++k) if (!hasSuccessor[k]) leaves.push_back(k);
+  Plan out;
+  for (size_t it = 0; it < iterations; ++it) {
+    size_t offset = out.nodes.size();
+    for (size_t k = 0; k < nodes.size(); ++k) {
+      std::vector<size_t> deps;
+      for (size_t d : nodes[k].dependencies) deps.push_back(offset + d);
+      if (it && nodes[k].dependencies.empty())
+        for (size_t leaf : leaves) deps.push_back(offset - nodes.size() + leaf);
+      out.addKernel(nodes[k].launch, std::move(deps));
+    }
+  }
+  return out;
+}
+
+GraphExec::~GraphExec() {
+  if (exec) hipGraphExecDestroy(exec);
+  if (graph) hipGraphDestroy(graph);
+}
+
+namespace {
+
+constexpr size_t kMaxGroup = 4;
+
+void launchOne(const Launch &launch, hipStream_t stream) {
+  void *params[] = {const_cast<uint8_t *>(launch.arguments.data())};
+  check(hipModuleLaunchKernel(launch.function, launch.grid[0], launch.grid[1], launch.grid[2], launch.block[0],
+                              launch.block[1], launch.block[2], launch.shared, stream, params, nullptr),
+        "hipModuleLaunchKernel");
+}
+
+void launchOrdinary(const Plan &plan, hipStream_t stream) {
+  for (const PlanNode &node : plan.nodes) launchOne(node.launch, stream);
+}
+
+// A unit of the inferred graph: one dispatch, or sibling dispatches of one library family
+// executed by the family's group entry point (each member keeps its own grid range).
+struct Unit {
+  std::vector<size_t> members;
+  Launch launch;
+};
+
+Launch groupLaunch(const Plan &plan, const std::vector<size_t> &members) {
+  const Launch &first = plan.nodes[members[0]].launch;
+  Launch out = first;
+  out.function = first.groupFunction;
+  out.groupFunction = nullptr;
+  size_t stride = first.arguments.size();
+  std::vector<uint8_t> blob(kMaxGroup * stride + 4 * (kMaxGroup + 1) + 4, 0);
+  int32_t start = 0;
+  std::vector<int32_t> starts;
+  for (size_t k = 0; k < members.size(); ++k) {
+    const Launch &m = plan.nodes[members[k]].launch;
+    std::memcpy(blob.data() + k * stride, m.arguments.data(), stride);
+    starts.push_back(start);
+    start += int32_t(m.grid[0]);
+  }
+  starts.push_back(start);
+  while (starts.size() < kMaxGroup + 1) starts.push_back(start);
+  std::memcpy(blob.data() + kMaxGroup * stride, starts.data(), 4 * (kMaxGroup + 1));
+  int32_t count = int32_t(members.size());
+  std::memcpy(blob.data() + kMaxGroup * stride + 4 * (kMaxGroup + 1), &count, 4);
+  blob.resize((blob.size() + 7) & ~size_t(7), 0);
+  out.arguments = std::move(blob);
+  out.grid[0] = unsigned(start);
+  return out;
+}
+
+std::vector<Unit> groupPlan(const Plan &plan) {
+  std::vector<size_t> level(plan.nodes.size(), 0);
+  size_t maxLevel = 0;
+  for (size_t k = 0; k < plan.nodes.size(); ++k) {
+    for (size_t d : plan.nodes[k].dependencies) level[k] = std::max(level[k], level[d] + 1);
+    maxLevel = std::max(maxLevel, level[k]);
+  }
+  std::vector<std::vector<size_t>> byLevel(maxLevel + 1);
+  for (size_t k = 0; k < plan.nodes.size(); ++k) byLevel[level[k]].push_back(k);
+  std::vector<Unit> units;
+  for (const auto &nodes : byLevel) {
+    std::vector<std::vector<size_t>> buckets;
+    for (size_t k : nodes) {
+      const Launch &l = plan.nodes[k].launch;
+      bool groupable = l.groupFunction && l.grid[1] == 1 && l.grid[2] == 1;
+      bool placed = false;
+      if (groupable)
+        for (auto &bucket : buckets) {
+          const Launch &b = plan.nodes[bucket[0]].launch;
+          if (bucket.size() < kMaxGroup && b.function == l.function && b.groupFunction &&
+              std::equal(b.block, b.block + 3, l.block) && b.shared == l.shared &&
+              b.arguments.size() == l.arguments.size() && b.grid[1] == 1 && b.grid[2] == 1) {
+            bucket.push_back(k);
+            placed = true;
+            break;
+          }
+        }
+      if (!placed) buckets.push_back({k});
+    }
+    for (auto &bucket : buckets) {
+      Unit u;
+      u.members = bucket;
+      u.launch = bucket.size() == 1 ? plan.nodes[bucket[0]].launch : groupLaunch(plan, bucket);
+      units.push_back(std::move(u));
+    }
+  }
+  return units;
+}
+
+std::unique_ptr<GraphExec> captureUnits(const std::vector<Launch> &launches, hipStream_t stream) {
+  auto out = std::make_unique<GraphExec>();
+  for (const Launch &l : launches) out->storage.push_back(l.arguments);
+  check(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+  try {
+    for (size_t k = 0; k < launches.size(); ++k) {
+      void *params[] = {out->storage[k].data()};
+      const Launch &l = launches[k];
+      check(hipModuleLaunchKernel(l.function, l.grid[0], l.grid[1], l.grid[2], l.block[0], l.block[1], l.block[2],
+                                  l.shared, stream, params, nullptr),
+            "hipModuleLaunchKernel(capture)");
+    }
+  } catch (...) {
+    hipGraph_t abandoned = nullptr;
+    hipStreamEndCapture(stream, &abandoned);
+    if (abandoned) hipGraphDestroy(abandoned);
+    throw;
+  }
+  check(hipStreamEndCapture(stream, &out->graph), "hipStreamEndCapture");
+  size_t count = 0;
+  check(hipGraphGetNodes(out->graph, nullptr, &count), "hipGraphGetNodes");
+  out->nodeCount = count;
+  check(hipGraphInstantiate(&out->exec, out->graph, nullptr, nullptr, 0), "hipGraphInstantiate(captured)");
+  return out;
+}
+
+// Explicit graph with one kernel node per unit and the units' dependency edges.
+std::unique_ptr<GraphExec> explicitGraph(const Plan &plan, const std::vector<Unit> &units) {
+  auto out = std::make_unique<GraphExec>();
+  std::vector<size_t> unitOf(plan.nodes.size());
+  for (size_t u = 0; u < units.size(); ++u) for (size_t m : units[u].members) unitOf[m] = u;
+  check(hipGraphCreate(&out->graph, 0), "hipGraphCreate");
+  std::vector<hipGraphNode_t> handles(units.size());
+  for (const Unit &u : units) out->storage.push_back(u.launch.arguments);
+  for (size_t u = 0; u < units.size(); ++u) {
+    std::vector<hipGraphNode_t> deps;
+    std::vector<size_t> seen;
+    for (size_t m : units[u].members)
+      for (size_t d : plan.nodes[m].dependencies) {
+        size_t du = unitOf[d];
+        if (du != u && std::find(seen.begin(), seen.end(), du) == seen.end()) { seen.push_back(du); deps.push_back(handles[du]); }
+      }
+    const Launch &l = units[u].launch;
+    void *params[] = {out->storage[u].data()};
+    hipKernelNodeParams p{};
+    p.func = reinterpret_cast<void *>(l.function);
+    p.gridDim = dim3(l.grid[0], l.grid[1], l.grid[2]);
+    p.blockDim = dim3(l.block[0], l.block[1], l.block[2]);
+    p.sharedMemBytes = l.shared;
+    p.kernelParams = params;
+    check(hipGraphAddKernelNode(&handles[u], out->graph, deps.data(), deps.size(), &p), "hipGraphAddKernelNode");
+  }
+  out->nodeCount = units.size();
+  check(hipGraphInstantiate(&out->exec, out->graph, nullptr, nullptr, 0), "hipGraphInstantiate");
+  return out;
+}
+
+} // namespace
+
+// ====================================================================== invocation
+Invocation::Invocation(std::shared_ptr<ProgramState> program_, std::shared_ptr<Device> device_)
+    : program(std::move(program_)), device(std::move(device_)) {
+  device->makeCurrent();
+  check(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "hipStreamCreateWithFlags");
+}
+
+Invocation::~Invocation() {
+  graphs.clear();
+  if (stream) {
+    device->makeCurrent();
+    hipStreamSynchronize(stream);
+    hipStreamDestroy(stream);
+  }
+}
+
+void Invocation::validate(int mode, uint64_t batch) const {
+  if (mode < 0 || mode > 2 || !batch || plan.nodes.empty() || batch > 1000000 / plan.nodes.size())
+    throw std::invalid_argument("invalid execution mode or batch exceeds one million kernel nodes");
+}
+
+GraphExec &Invocation::graphFor(int mode, uint64_t batch) {
+  auto &slot = graphs[{mode, batch}];
+  if (!slot) {
+    Plan repeated = batch == 1 ? plan : plan.repeat(batch);
+    if (mode == 2) {
+      std::vector<Launch> launches;
+      for (const PlanNode &n : repeated.nodes) launches.push_back(n.launch);
+      slot = captureUnits(launches, stream);
+    } else if (branchPolicy() == BranchPolicy::Branches) {
+      std::vector<Unit> units;
+      for (size_t k = 0; k < repeated.nodes.size(); ++k) units.push_back({{k}, repeated.nodes[k].launch});
+      slot = explicitGraph(repeated, units);
+    } else {
+      // Sibling groups ordered by DAG level, captured as one chain of launches.
+      std::vector<Unit> units = groupPlan(repeated);
+      std::vector<Launch> launches;
+      for (const Unit &u : units) launches.push_back(u.launch);
+      slot = captureUnits(launches, stream);
+    }
+  }
+  return *slot;
+}
+
+void Invocation::execute(int mode, uint64_t batch) {
+  device->makeCurrent();
+  if (mode) {
+    check(hipGraphLaunch(graphFor(mode, batch).exec, stream), "hipGraphLaunch");
+  } else {
+    for (uint64_t k = 0; k < batch; ++k) launchOrdinary(plan, stream);
+  }
+}
+
+size_t Invocation::graphNodeCount(int mode, uint64_t batch) {
+  std::lock_guard<std::mutex> lock(runMutex);
+  validate(mode, batch);
+  if (!mode) return plan.nodes.size() * batch;
+  return graphFor(mode, batch).nodeCount;
+}
+
+void Invocation::run(int mode, uint64_t batch) {
+  std::lock_guard<std::mutex> lock(runMutex);
+  validate(mode, batch);
+  execute(mode, batch);
+  check(hipStreamSynchronize(stream), "hipStreamSynchronize");
+}
+
+std::array<double, 3> Invocation::benchmark(int mode, uint64_t iterations, uint64_t batch) {
+  if (!iterations) throw std::invalid_argument("benchmark iterations must be positive");
+  std::lock_guard<std::mutex> lock(runMutex);
+  validate(mode, batch);
+  std::array<double, 3> result{};
+  using Clock = std::chrono::steady_clock;
+  device->makeCurrent();
+  check(hipStreamSynchronize(stream), "hipStreamSynchronize");
+  auto setup = Clock::now();
+  if (mode) graphFor(mode, batch);
+  result[2] = std::chrono::duration<double, std::milli>(Clock::now() - setup).count();
+  hipEvent_t start = nullptr, stop = nullptr;
+  check(hipEventCreate(&start), "hipEventCreate");
+  try {
+    check(hipEventCreate(&stop), "hipEventCreate");
+    check(hipEventRecord(start, stream), "hipEventRecord");
+    auto wall = Clock::now();
+    for (uint64_t k = 0; k < iterations; ++k) execute(mode, batch);
+    check(hipEventRecord(stop, stream), "hipEventRecord");
+    check(hipEventSynchronize(stop), "hipEventSynchronize");
+    auto wallStop = Clock::now();
+    float elapsed = 0;
+    check(hipEventElapsedTime(&elapsed, start, stop), "hipEventElapsedTime");
+    result[0] = double(elapsed) * 1000.0 / double(iterations) / double(batch);
+    result[1] = std::chrono::duration<double, std::micro>(wallStop - wall).count() / double(iterations) / double(batch);
+  } catch (...) {
+    hipEventDestroy(start);
+    if (stop) hipEventDestroy(stop);
+    throw;
+  }
+  hipEventDestroy(start);
+  hipEventDestroy(stop);
+  return result;
+}
+
+// ====================================================================== callbacks
+// The callback protocol of lib/Runtime/NvidiaProgram.cpp:48-108: exceptions never unwind
+// through the entry; the first failure is recorded and later callbacks become no-ops.
+template <typename F> static void callback(void *opaque, F action) {
+  auto &frame = *static_cast<Invocation *>(opaque);
+  if (!frame.error.empty()) return;
+  try {
+    action(frame);
+  } catch (const std::exception &error) {
+    frame.error = error.what();
+    if (frame.error.empty()) frame.error = "callback failed";
+  }
+}
+
+static void appendArgument(Launch &launch, const void *data, uint64_t size) {
+  if (!data || !size) throw std::invalid_argument("physical kernel argument must not be empty");
+  size_t align = (size == 1 || size == 2 || size == 4 || size == 8) ? size : 1;
+  size_t offset = (launch.arguments.size() + align - 1) & ~(align - 1);
+  launch.arguments.resize(offset + size, 0);
+  std::memcpy(launch.arguments.data() + offset, data, size);
+  launch.slotOffsets.push_back(offset);
+}
+
+std::shared_ptr<Invocation> bind(const std::shared_ptr<ProgramState> &programIn, std::shared_ptr<Device> device,
+                                 const std::vector<Argument> &arguments) {
+  auto program = programIn;
+  if (!device) throw std::invalid_argument("program binding requires a device");
+  size_t count = arguments.size();
+  if (count != program->bufferBytes.size()) throw std::invalid_argument("incorrect program argument count");
+  std::vector<uint64_t> addresses(count), scalars(count);
+  std::vector<void *> packed(count);
+  std::vector<std::shared_ptr<Buffer>> buffers;
+  for (size_t k = 0; k < count; ++k) {
+    const Argument &a = arguments[k];
+    if (program->bufferBytes[k]) {
+      if (a.kind != 0 || !a.buffer || a.buffer->device != device || a.buffer->bytes < program->bufferBytes[k])
+        throw std::invalid_argument("buffer device or size does not match compiled signature");
+      addresses[k] = a.buffer->address();
+      packed[k] = &addresses[k];
+      buffers.push_back(a.buffer);
+    } else {
+      const std::string &type = program->scalarTypes[k];
+      auto store = [&](auto value) { std::memcpy(&scalars[k], &value, sizeof(value)); };
+      if (type == "i32" && a.kind == 1) store(int32_t(a.integer));
+      else if (type == "i64" && a.kind == 2) store(int64_t(a.integer));
+      else if (type == "f32" && a.kind == 3) store(float(a.real));
+      else if (type == "f64" && a.kind == 4) store(double(a.real));
+      else throw std::invalid_argument("argument type does not match compiled signature");
+      packed[k] = &scalars[k];
+    }
+  }
+  // Fused programs fall back to their unfused form when external byte ranges overlap
+  // (lib/Runtime/NvidiaProgram.cpp:191-205).
+  if (program->aliasFallback) {
+    bool overlap = false;
+    for (size_t i = 0; i < count; ++i)
+      for (size_t j = i + 1; j < count; ++j) {
+        if (!program->bufferBytes[i] || !program->bufferBytes[j]) continue;
+        overlap |= addresses[i] <= addresses[j] ? addresses[j] - addresses[i] < program->bufferBytes[i]
+                                                : addresses[i] - addresses[j] < program->bufferBytes[j];
+      }
+    if (overlap) program = program->aliasFallback;
+  }
+  auto invocation = std::make_shared<Invocation>(program, device);
+  invocation->buffers = std::move(buffers);
+  void *frame = invocation.get();
+  void **values = packed.data();
+  void *entryArguments[] = {&frame, &values, program->entryContext};
+  program->entry(entryArguments);
+  if (!invocation->error.empty()) throw std::runtime_error(invocation->error);
+  return invocation;
+}
+
+} // namespace ckl::rt
+
+using ckl::rt::Invocation;
+using ckl::rt::Launch;
+
+extern "C" void ckl_begin(void *frame, const void *binary, uint64_t bytes) {
+  ckl_module(frame, "", binary, bytes);
+}
+
+extern "C" void ckl_module(void *frame, const char *identity, const void *binary, uint64_t bytes) {
+  ckl::rt::callback(frame, [&](Invocation &f) {
+    std::string key = identity && *identity ? identity : "program:" + std::to_string(reinterpret_cast<uintptr_t>(f.program.get()));
+    f.module = f.device->load(key, binary, bytes);
+  });
+}
+
+extern "C" void ckl_heap(void *frame, uint64_t id, uint64_t bytes) {
+  ckl::rt::callback(frame, [&](Invocation &f) {
+    if (f.heaps.size() <= id) f.heaps.resize(id + 1);
+    f.heaps[id] = ckl::rt::allocateBuffer(f.device, bytes);
+  });
+}
+
+extern "C" void ckl_resource(void *frame, uint64_t id, uint64_t heap, uint64_t offset, void *external) {
+  ckl::rt::callback(frame, [&](Invocation &f) {
+    if (f.resources.size() <= id) f.resources.resize(id + 1);
+    if (external) f.resources[id] = *static_cast<uint64_t *>(external);
+    else {
+      const auto &h = f.heaps.at(heap);
+      if (!h || offset > h->bytes) throw std::out_of_range("resource placement exceeds its heap");
+      f.resources[id] = h->address() + offset;
+    }
+  });
+}
+
+extern "C" void ckl_kernel(void *frame, const char *name, uint64_t gx, uint64_t gy, uint64_t gz, uint64_t bx,
+                           uint64_t by, uint64_t bz, uint64_t shared) {
+  ckl::rt::callback(frame, [&](Invocation &f) {
+    if (!f.module) throw std::invalid_argument("ckl_kernel requires a loaded module (ckl_begin)");
+    Launch launch;
+    launch.name = name;
+    ckl::rt::check(hipModuleGetFunction(&launch.function, f.module, name), "hipModuleGetFunction");
+    hipFunction_t group = nullptr;
+    std::string groupName = std::string(name) + "_group";
+    if (hipModuleGetFunction(&group, f.module, groupName.c_str()) == hipSuccess) launch.groupFunction = group;
+    else (void)hipGetLastError();
+    uint64_t dims[6] = {gx, gy, gz, bx, by, bz};
+    for (uint64_t d : dims)
+      if (!d || d > 0xffffffffull) throw std::invalid_argument("kernel launch dimensions must be positive 32-bit values");
+    launch.grid[0] = unsigned(gx); launch.grid[1] = unsigned(gy); launch.grid[2] = unsigned(gz);
+    launch.block[0] = unsigned(bx); launch.block[1] = unsigned(by); launch.block[2] = unsigned(bz);
+    launch.shared = unsigned(shared);
+    f.pending = std::move(launch);
+    f.dependencies.clear();
+  });
+}
+
+extern "C" void ckl_argument_resource(void *frame, uint64_t id, uint64_t offset) {
+  ckl::rt::callback(frame, [&](Invocation &f) {
+    uint64_t address = f.resources.at(id) + offset;
+    ckl::rt::appendArgument(f.pending, &address, sizeof address);
+  });
+}
+
+extern "C" void ckl_argument_value(void *frame, const void *bytes, uint64_t size) {
+  ckl::rt::callback(frame, [&](Invocation &f) { ckl::rt::appendArgument(f.pending, bytes, size); });
+}
+
+extern "C" void ckl_dependency(void *frame, uint64_t id) {
+  ckl::rt::callback(frame, [&](Invocation &f) { f.dependencies.push_back(f.nodes.at(id)); });
+}
+
+extern "C" void ckl_commit(void *frame, uint64_t id) {
+  ckl::rt::callback(frame, [&](Invocation &f) {
+    f.pending.arguments.resize((f.pending.arguments.size() + 7) & ~size_t(7), 0);
+    if (f.pending.arguments.empty()) f.pending.arguments.resize(8, 0);
+    f.nodes[id] = f.plan.addKernel(std::move(f.pending), std::move(f.dependencies));
+    f.pending = Launch();
+    f.dependencies.clear();
+  });
+}

@@ -1,0 +1,148 @@
+// HIP executor for CKL executable plans on MI355X (gfx950).
+//
+// Replaces the reference's CUDA driver executor and program layer:
+//   lib/Runtime/NvidiaRuntime.cpp:177-498   plans, repeat, ordinary launch, capture, explicit graphs
+//   lib/Runtime/NvidiaProgram.cpp:13-294    callback ABI, bind, run, benchmark
+//   lib/Runtime/HipRuntime.cpp:212-466      hipModule loading and kernel nodes
+// Execution modes: 0 ordinary launches, 1 inferred graph (from the plan's dependency DAG),
+// 2 single-stream capture of ordinary launches.
+#pragma once
+
+#include "callbacks.h"
+
+#include <hip/hip_runtime.h>
+
+#include <array>
+#include <atomic>
+#include <cstdint>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <vector>
+
+namespace ckl::rt {
+
+void check(hipError_t status, const char *what);
+
+struct Device {
+  explicit Device(int ordinal);
+  ~Device();
+  int ordinal;
+  uint64_t id;
+  std::string name;
+  std::mutex moduleMutex;
+  std::map<std::string, hipModule_t> modules;   // artifact identity -> loaded module
+  hipModule_t load(const std::string &identity, const void *image, size_t bytes);
+  void makeCurrent() const;
+};
+
+struct Buffer {
+  std::shared_ptr<Device> device;
+  std::shared_ptr<void> storage;   // owning allocation (null for imports)
+  uint64_t base = 0;               // address of the underlying allocation/import
+  uint64_t offset = 0;
+  uint64_t bytes = 0;
+  uint64_t address() const { return base + offset; }
+  void copyFromHost(const void *data, uint64_t size) const;
+  void copyToHost(void *data, uint64_t size) const;
+};
+
+std::shared_ptr<Buffer> allocateBuffer(std::shared_ptr<Device> device, uint64_t bytes);
+std::shared_ptr<Buffer> importBuffer(std::shared_ptr<Device> device, uint64_t address, uint64_t bytes);
+std::shared_ptr<Buffer> sliceBuffer(const std::shared_ptr<Buffer> &buffer, uint64_t offset, uint64_t bytes);
+
+// One resolved kernel launch: function, geometry and the packed argument struct.
+struct Launch {
+  hipFunction_t function = nullptr;
+  hipFunction_t groupFunction = nullptr;   // sibling-group entry point, when the artifact has one
+  std::string name;
+  unsigned grid[3] = {1, 1, 1};
+  unsigned block[3] = {1, 1, 1};
+  unsigned shared = 0;
+  std::vector<uint8_t> arguments;           // kernarg bytes (natural alignment, padded to 8)
+  std::vector<size_t> slotOffsets;
+};
+
+struct PlanNode {
+  Launch launch;
+  std::vector<size_t> dependencies;         // earlier plan nodes
+};
+
+struct Plan {
+  std::vector<PlanNode> nodes;
+  size_t addKernel(Launch launch, std::vector<size_t> dependencies);
+  Plan repeat(size_t iterations) const;      // roots of iteration i+1 follow every leaf of i
+};
+
+struct GraphExec {
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  size_t nodeCount = 0;
+  std::vector<std::vector<uint8_t>> storage;   // kernarg blocks referenced during capture
+  ~GraphExec();
+};
+
+struct ProgramState;
+
+// Invocation: a bound program with its stream, heaps, resolved plan and cached graphs.
+struct Invocation {
+  std::shared_ptr<ProgramState> program;
+  std::shared_ptr<Device> device;
+  hipStream_t stream = nullptr;
+  std::vector<std::shared_ptr<Buffer>> heaps;
+  std::vector<std::shared_ptr<Buffer>> buffers;     // keeps bound buffers alive
+  std::vector<uint64_t> resources;
+  Plan plan;
+  hipModule_t module = nullptr;                     // current module during plan construction
+  Launch pending;
+  std::vector<size_t> dependencies;
+  std::map<uint64_t, size_t> nodes;                 // graph node id -> plan node
+  std::map<std::pair<int, uint64_t>, std::unique_ptr<GraphExec>> graphs;
+  std::mutex runMutex;
+  std::string error;
+
+  Invocation(std::shared_ptr<ProgramState> program, std::shared_ptr<Device> device);
+  ~Invocation();
+  void run(int mode, uint64_t batch);
+  std::array<double, 3> benchmark(int mode, uint64_t iterations, uint64_t batch);
+  size_t nodeCount() const { return plan.nodes.size(); }
+  size_t graphNodeCount(int mode, uint64_t batch);
+
+private:
+  void validate(int mode, uint64_t batch) const;
+  GraphExec &graphFor(int mode, uint64_t batch);
+  void execute(int mode, uint64_t batch);
+};
+
+using Entry = void (*)(void **);
+
+// Program: metadata for a packed host entry that builds the plan through the callback ABI.
+struct ProgramState {
+  Entry entry = nullptr;
+  void *entryContext = nullptr;                     // native entries: the compiled plan
+  std::vector<uint64_t> bufferBytes;
+  std::vector<std::string> scalarTypes;
+  std::shared_ptr<ProgramState> aliasFallback;
+  std::shared_ptr<void> owner;                      // keeps compiled state alive
+};
+
+struct Argument {
+  int kind = 0;                 // 0 buffer, 1 i32, 2 i64, 3 f32, 4 f64
+  std::shared_ptr<Buffer> buffer;
+  int64_t integer = 0;
+  double real = 0;
+};
+
+std::shared_ptr<Invocation> bind(const std::shared_ptr<ProgramState> &program, std::shared_ptr<Device> device,
+                                 const std::vector<Argument> &arguments);
+
+// Graph policy for mode 1: group sibling dispatches of one library family into one launch and
+// chain the result (default), or keep one graph node per dispatch with real branches.
+enum class BranchPolicy { Grouped, Branches };
+BranchPolicy branchPolicy();
+
+int deviceCount();
+
+} // namespace ckl::rt
+

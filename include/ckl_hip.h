@@ -1,0 +1,138 @@
+/*
+ * ckl_hip.h — C ABI of the MI355X (gfx950) CKL backend: compiler pipeline, HIP executor
+ * and the host-entry callback protocol.
+ *
+ * This ABI replaces the reference's native boundary for the decode hot path:
+ *   - the nanobind module `_ckl_native` (lib/Compiler/RuntimeBindings.cpp:56-105,
+ *     lib/Compiler/NativeBindings.cpp:23-61) that python/ckl/cuda.py and python/ckl/_jit.py call;
+ *   - the C++ program API (include/ckl/Runtime/NvidiaProgram.h:16-69);
+ *   - the eight JIT->runtime callbacks (lib/Runtime/NvidiaProgram.cpp:60-108).
+ * Plain pointers and sizes only. Every function returning int returns CKL_OK (0) on success;
+ * on failure ckl_last_error() holds a thread-local message and the code tells the Python layer
+ * which exception to raise (ValueError for CKL_INVALID_ARGUMENT, RuntimeError otherwise).
+ */
+#ifndef CKL_HIP_H
+#define CKL_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  CKL_OK = 0,
+  CKL_INVALID_ARGUMENT = 1, /* std::invalid_argument / out_of_range -> ValueError */
+  CKL_RUNTIME_ERROR = 2,    /* HIP or runtime failure -> RuntimeError */
+  CKL_COMPILE_ERROR = 3     /* IR, analysis or device compilation failure -> RuntimeError */
+};
+
+typedef struct ckl_program ckl_program;
+typedef struct ckl_device ckl_device;
+typedef struct ckl_buffer ckl_buffer;
+typedef struct ckl_invocation ckl_invocation;
+
+/* Version of this ABI; bumped on any incompatible change. */
+int ckl_abi_version(void);
+/* Message of the last failed call on this thread (empty when none). */
+const char *ckl_last_error(void);
+/* Releases strings returned through `char **` out-parameters. */
+void ckl_string_free(char *text);
+
+/* ---------------------------------------------------------------- compiler
+ * Replaces python/ckl/_jit.py:74-154 (compile_program: fuse, prepare, build-graph,
+ * lower-graph-to-exec, device and host lowering) and `make_program`
+ * (lib/Compiler/RuntimeBindings.cpp:61-67). `ir` is CKL IR text as printed by the frontend. */
+typedef struct {
+  int reuse_storage;   /* graph-order temporary reuse (GraphAnalysis.cpp:610-612) */
+  int fuse_pointwise;  /* guarded unary pointwise fusion (PointwiseFusion.cpp:260-304) */
+  int strict;          /* reject operations without complete effect semantics */
+  const char *chip;    /* "gfx950" */
+} ckl_compile_options;
+
+int ckl_compile(const char *ir, const ckl_compile_options *options, ckl_program **out);
+/* IR views of CompiledProgram (python/ckl/cuda.py:189-208):
+ * 0 prepared IR, 1 executable plan IR, 2 device code (generated HIP source),
+ * 3 host entry call sequence, 4 host entry call sequence of the unfused fallback ("" if none).
+ * The text is owned by the program. */
+int ckl_program_ir(ckl_program *program, int stage, const char **text, size_t *size);
+/* Host signature derived from the program (bufferBytes / scalarTypes of NvidiaProgram.h:44-48):
+ * for argument k, bytes[k] > 0 for a buffer, else types[k] is "i32", "i64", "f32" or "f64". */
+int ckl_program_signature(ckl_program *program, size_t *count, const uint64_t **bytes, const char *const **types);
+/* A program whose plan is built by an external packed entry `entry(void*[]{&frame, &values})`
+ * driving the callbacks below (NvidiaProgram::NvidiaProgram, NvidiaProgram.cpp:136-146). */
+int ckl_program_from_entry(void (*entry)(void **), const uint64_t *buffer_bytes, const char *const *scalar_types,
+                           size_t count, ckl_program *fallback, ckl_program **out);
+void ckl_program_release(ckl_program *program);
+
+/* ckl-opt style pass pipeline over IR text (tools/ckl-opt/ckl-opt.cpp:1-29): `passes` is a
+ * comma-free list separated by ';', e.g. "build-graph;lower-graph-to-exec". */
+int ckl_opt(const char *ir, const char *passes, char **out);
+
+/* Identity of the hand-written gfx950 kernel library code object ("" when absent). */
+const char *ckl_library_identity(void);
+
+/* ---------------------------------------------------------------- runtime
+ * Replaces `cuda_available`, `Device`, `Buffer`, `bind` and `Invocation`
+ * (lib/Compiler/RuntimeBindings.cpp:18-105; python/ckl/cuda.py:93-300). */
+int ckl_device_count(void);
+int ckl_device_open(int ordinal, ckl_device **out);
+const char *ckl_device_name(ckl_device *device);
+void ckl_device_release(ckl_device *device);
+
+int ckl_buffer_alloc(ckl_device *device, uint64_t bytes, ckl_buffer **out);
+/* Borrows caller-owned device memory (Device.import_buffer, cuda.py:115-122). */
+int ckl_buffer_import(ckl_device *device, uint64_t address, uint64_t bytes, ckl_buffer **out);
+int ckl_buffer_slice(ckl_buffer *buffer, uint64_t offset, uint64_t bytes, ckl_buffer **out);
+uint64_t ckl_buffer_address(ckl_buffer *buffer);
+uint64_t ckl_buffer_nbytes(ckl_buffer *buffer);
+/* Synchronous copies; complete before any later launch on any stream (cuda.py:154-164). */
+int ckl_buffer_copy_from_host(ckl_buffer *buffer, const void *data, uint64_t bytes);
+int ckl_buffer_copy_to_host(ckl_buffer *buffer, void *data, uint64_t bytes);
+void ckl_buffer_release(ckl_buffer *buffer);
+
+enum { CKL_ARG_BUFFER = 0, CKL_ARG_I32 = 1, CKL_ARG_I64 = 2, CKL_ARG_F32 = 3, CKL_ARG_F64 = 4 };
+typedef struct {
+  int kind;
+  ckl_buffer *buffer;
+  int64_t integer;
+  double real;
+} ckl_argument;
+
+/* NvidiaProgram::bind (NvidiaProgram.cpp:156-215): packs arguments, selects the unfused
+ * fallback when external byte ranges overlap, runs the host entry and returns the bound
+ * invocation (one stream, one allocation per planned heap). */
+int ckl_bind(ckl_program *program, ckl_device *device, const ckl_argument *arguments, size_t count,
+             ckl_invocation **out);
+/* mode: 0 ordinary launches, 1 inferred graph, 2 single-stream capture (NvidiaProgram.h:327-330).
+ * Synchronizes the invocation stream before returning. */
+int ckl_invocation_run(ckl_invocation *invocation, int mode, uint64_t batch);
+/* out[0] stream us/step, out[1] wall us/step, out[2] graph setup ms (NvidiaProgram.cpp:225-270). */
+int ckl_invocation_benchmark(ckl_invocation *invocation, int mode, uint64_t iterations, uint64_t batch, double out[3]);
+uint64_t ckl_invocation_node_count(ckl_invocation *invocation);
+/* Number of device launches (graph nodes) one execution of `batch` steps submits in `mode`. */
+int ckl_invocation_launch_count(ckl_invocation *invocation, int mode, uint64_t batch, uint64_t *count);
+void ckl_invocation_release(ckl_invocation *invocation);
+
+/* ---------------------------------------------------------------- host-entry callbacks
+ * The reference's eight callbacks with identical signatures (NvidiaProgram.cpp:60-108) plus
+ * ckl_module, which loads (once per device) and selects a named code object so one plan can
+ * mix library kernels and JIT-compiled kernels. Errors are recorded in `frame`; later
+ * callbacks become no-ops and ckl_bind reports the first error. */
+void ckl_begin(void *frame, const void *binary, uint64_t bytes);
+void ckl_module(void *frame, const char *identity, const void *binary, uint64_t bytes);
+void ckl_heap(void *frame, uint64_t id, uint64_t bytes);
+void ckl_resource(void *frame, uint64_t id, uint64_t heap, uint64_t offset, void *external);
+void ckl_kernel(void *frame, const char *name, uint64_t gx, uint64_t gy, uint64_t gz, uint64_t bx, uint64_t by,
+                uint64_t bz, uint64_t shared);
+void ckl_argument_resource(void *frame, uint64_t id, uint64_t offset);
+void ckl_argument_value(void *frame, const void *bytes, uint64_t size);
+void ckl_dependency(void *frame, uint64_t id);
+void ckl_commit(void *frame, uint64_t id);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CKL_HIP_H */
