@@ -65,7 +65,7 @@ def build_kernels() -> None:
     output = OUT / f"ckl_kernels_{ARCH}.hsaco"
     tmp = output.with_suffix(".hsaco.tmp")
     sources = [str(CSRC / s) for s in KERNEL_SOURCES]
-    run([str(ROCM / "bin" / "hipcc"), "--genco", f"--offload-arch={ARCH}", "-O3", "-std=c++17",
+    run([str(ROCM / "bin" / "hipcc"), "--genco", "--no-gpu-bundle-output", f"--offload-arch={ARCH}", "-O3", "-std=c++17",
          *DEVICE_FLAGS, "-o", str(tmp), *sources])
     os.replace(tmp, output)
 

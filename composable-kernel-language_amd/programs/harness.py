@@ -1,0 +1,158 @@
+"""Device-side harness for the decoder workload: synthetic inputs, device state with sentinel
+tails, compile/bind of the storage ablation, GPU prefill, and state verification.
+
+The verification protocol is that of benchmarks/decoder/run.py:81-132 in the reference:
+256-element sentinel tails after every buffer, exact integer state (tokens, history,
+position), f32 state within atol 2e-5 / rtol 3e-4, unchanged weights, and unchanged KV-cache
+prefix and suffix outside the positions a run writes.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+import ckl
+from programs.decoder import decode
+from programs.decoder_config import EPSILON, MUTABLE, Config, shapes, signature
+
+TAIL = 256
+SENTINEL = -12345
+WEIGHTS = ("emb", "norm1", "norm2", "final_norm", "wq", "wk", "wv", "wo", "wg", "wu", "wd", "lm")
+
+
+def synthetic_inputs(c: Config, seed: int = 123, *, init: str = "baseline"):
+    """Seeded weights, RoPE table, prompts and empty persistent state (no prefill).
+
+    Draw order and distributions: weights in WEIGHTS order from default_rng(seed) (gains
+    1 + N(0, 0.02); embedding and matrices N(0, 0.02) for init="baseline", or N(0, 0.5) and
+    N(0, 0.5/sqrt(fan_in)) for init="reference"), then prompts integers(0, V, (context, B)).
+    """
+    rng = np.random.default_rng(seed)
+    sh = shapes(c)
+    arrays = {}
+    for name in WEIGHTS:
+        shape = sh[name][0]
+        if "norm" in name:
+            arrays[name] = (1 + rng.normal(0, 0.02, shape)).astype(np.float32)
+        elif init == "baseline":
+            arrays[name] = rng.normal(0, 0.02, shape).astype(np.float32)
+        elif init == "reference":
+            arrays[name] = rng.normal(0, 0.5 if name == "emb" else 0.5 / np.sqrt(shape[-2]), shape).astype(np.float32)
+        else:
+            raise ValueError(f"unknown init {init!r}")
+    d, t = c.head_dim, c.capacity
+    angles = np.arange(t)[:, None] * (10000. ** (-np.arange(0, d, 2) / d))[None, :]
+    arrays["sincos"] = np.stack((np.cos(angles), np.sin(angles)), axis=-1).astype(np.float32)
+    prompts = rng.integers(0, c.vocab, (c.context, c.batch), dtype=np.int32)
+    arrays.update(tokens=prompts[0].copy(), position=np.array([0], dtype=np.int32),
+                  history=np.full(sh["history"][0], -1, dtype=np.int32),
+                  kc=np.full(sh["kc"][0], SENTINEL, dtype=np.float32),
+                  vc=np.full(sh["vc"][0], SENTINEL, dtype=np.float32),
+                  logits=np.full(sh["logits"][0], SENTINEL, dtype=np.float32))
+    return arrays, prompts
+
+
+class DecoderState:
+    """Device copies of every program argument, each followed by a sentinel tail."""
+
+    def __init__(self, device: ckl.Device, c: Config, arrays: dict):
+        self.device, self.config = device, c
+        self.initial = {k: v for k, v in arrays.items()}
+        self.owners, self.buffers, self.host = {}, {}, {}
+        for name, (shape, dtype) in shapes(c).items():
+            values = arrays[name]
+            if tuple(values.shape) != tuple(shape):
+                raise ValueError(f"{name}: shape {values.shape} != {shape}")
+            host = np.full(values.size + TAIL, SENTINEL, dtype=values.dtype)
+            host[:values.size] = values.ravel()
+            kind = ckl.i32 if dtype == "i32" else ckl.f32
+            owner = device.empty(ckl.BufferSpec(host.shape, kind))
+            owner.copy_from_host(host)
+            self.owners[name], self.host[name] = owner, host
+            self.buffers[name] = device.import_buffer(owner.address, ckl.BufferSpec(tuple(shape), kind), owner=owner)
+
+    def arguments(self):
+        c = self.config
+        args = [self.buffers[name] for name in shapes(c)]
+        return args + [float(np.float32(EPSILON)), float(c.head_dim ** -0.5)]
+
+    def reset(self, names=MUTABLE):
+        for name in names:
+            self.owners[name].copy_from_host(self.host[name])
+
+    def set_tokens(self, tokens: np.ndarray):
+        self.buffers["tokens"].copy_from_host(np.ascontiguousarray(tokens, dtype=np.int32))
+
+    def download(self, name: str, *, with_tail=False) -> np.ndarray:
+        out = np.empty_like(self.host[name])
+        self.owners[name].copy_to_host(out)
+        if with_tail:
+            return out
+        return out[:self.initial[name].size].reshape(self.initial[name].shape)
+
+    def snapshot(self):
+        """Make the current device state the reset point (after a device prefill)."""
+        for name in MUTABLE:
+            full = self.download(name, with_tail=True)
+            self.host[name] = full
+            self.initial[name] = full[:self.initial[name].size].reshape(self.initial[name].shape).copy()
+
+    def verify(self, reference: dict, *, check_weights=True) -> float:
+        """Compare device state with `reference` (arrays after the same steps). Returns the
+        maximum f32 error; raises AssertionError on any violation."""
+        errors = {}
+        start, end = int(self.initial["position"][0]), int(reference["position"][0])
+        for name in shapes(self.config):
+            if name not in MUTABLE and not check_weights:
+                continue
+            actual = self.download(name, with_tail=True)
+            size = self.initial[name].size
+            if not np.all(actual[size:] == SENTINEL):
+                raise AssertionError(f"{name}: tail overwritten")
+            actual = actual[:size].reshape(self.initial[name].shape)
+            if name not in MUTABLE:
+                if not np.array_equal(actual, self.initial[name]):
+                    raise AssertionError(f"{name}: model weights/input metadata changed")
+            elif actual.dtype == np.int32:
+                if not np.array_equal(actual, reference[name]):
+                    raise AssertionError(f"{name}: token/history/position mismatch\n{actual}\n{reference[name]}")
+            else:
+                if not np.all(np.isfinite(actual)) or not np.allclose(actual, reference[name], atol=2e-5, rtol=3e-4):
+                    raise AssertionError(f"{name}: numerical mismatch, max error {np.max(np.abs(actual - reference[name]))}")
+                errors[name] = float(np.max(np.abs(actual - reference[name])))
+                if name in ("kc", "vc"):
+                    if not np.array_equal(actual[:, :, :, :start], self.initial[name][:, :, :, :start]):
+                        raise AssertionError(f"{name}: prefilled cache changed")
+                    if not np.array_equal(actual[:, :, :, end:], self.initial[name][:, :, :, end:]):
+                        raise AssertionError(f"{name}: unused cache suffix changed")
+        return max(errors.values(), default=0.0)
+
+
+class DecoderSession:
+    """Lowered decode program compiled with storage reuse off and on, bound to one state."""
+
+    def __init__(self, c: Config, device: ckl.Device = None, *, arrays=None, seed=123, init="baseline"):
+        self.config = c
+        self.device = device or ckl.Device()
+        if arrays is None:
+            arrays, self.prompts = synthetic_inputs(c, seed, init=init)
+        else:
+            self.prompts = None
+        self.lowered = decode.lower(signature=signature(c))
+        self.programs = {reuse: self.lowered.compile(fuse_pointwise=False, reuse_storage=reuse) for reuse in (False, True)}
+        self.state = DecoderState(self.device, c, arrays)
+        self.invocations = {reuse: p.bind(*self.state.arguments()) for reuse, p in self.programs.items()}
+        expected_nodes = 21 * c.layers + 6
+        for inv in self.invocations.values():
+            if inv.node_count != expected_nodes:
+                raise AssertionError("unexpected decoder dispatch count")
+        if self.programs[False].prepared_ir != self.programs[True].prepared_ir:
+            raise AssertionError("storage ablation changed the prepared device kernels")
+
+    def prefill(self, prompts: np.ndarray, *, mode="graph"):
+        """Teacher-forced device prefill of context-1 steps (reference.py:102-106 semantics):
+        each step runs the decode program, then the next prompt token replaces the argmax."""
+        inv = self.invocations[True]
+        for i in range(self.config.context - 1):
+            inv.run(mode=mode)
+            self.state.set_tokens(prompts[i + 1])
+        self.state.snapshot()

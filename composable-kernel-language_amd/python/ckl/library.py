@@ -234,17 +234,17 @@ def _elementwise(count: int, inner: int) -> int:
 
 
 def _embedding(shapes, consts, ext):
-    (b,), (v, c), _ = shapes
+    (b,), (v, c) = shapes[0], shapes[1]
     return Launch(_elementwise(b * c, c), (b, c, v)) if ext[0] >= c and ext[1:] == (b, 1) else None
 
 
 def _rms_stats(shapes, consts, ext):
-    (b, c), _, _ = shapes
+    b, c = shapes[0]
     return Launch(_cdiv(b, 4), (b, c)) if ext[0] >= b and ext[1:] == (1, 1) else None
 
 
 def _rms_apply(shapes, consts, ext):
-    (b, c), _, (g, _c), _ = shapes
+    (b, c), (g, _c) = shapes[0], shapes[2]
     layer = consts[4]
     if not (0 <= layer < g) or not (ext[0] >= c and ext[1:] == (b, 1)):
         return None
@@ -252,7 +252,7 @@ def _rms_apply(shapes, consts, ext):
 
 
 def _linear(shapes, consts, ext):
-    (b, i), (w, _i, o), _ = shapes
+    (b, i), (w, _i, o) = shapes[0], shapes[1]
     layer = consts[3]
     if not (0 <= layer < w) or not (ext[0] >= o and ext[1:] == (b, 1)):
         return None
@@ -260,7 +260,7 @@ def _linear(shapes, consts, ext):
 
 
 def _rope(shapes, consts, ext):
-    (b, c), (t, r, _two), _, _ = shapes
+    (b, c), (t, r, _two) = shapes[0], shapes[1]
     if c % (2 * r):
         return None
     a = c // (2 * r)
@@ -270,7 +270,7 @@ def _rope(shapes, consts, ext):
 
 
 def _append_kv(shapes, consts, ext):
-    (b, c), _, (l, _b, a, t, d), _, _ = shapes
+    (b, c), (l, _b, a, t, d) = shapes[0], shapes[2]
     layer = consts[5]
     if a * d != c or not (0 <= layer < l) or not (ext[0] >= d and ext[1:] == (a, b)):
         return None
@@ -278,7 +278,7 @@ def _append_kv(shapes, consts, ext):
 
 
 def _scores(shapes, consts, ext):
-    (b, c), (l, _b, a, t, d), _, _, _ = shapes
+    (b, c), (l, _b, a, t, d) = shapes[0], shapes[1]
     layer = consts[5]
     if a * d != c or not (0 <= layer < l) or not (ext[0] >= t and ext[1:] == (a, b)):
         return None
@@ -286,14 +286,14 @@ def _scores(shapes, consts, ext):
 
 
 def _softmax(shapes, consts, ext):
-    (b, a, t), _, _ = shapes
+    b, a, t = shapes[0]
     if not (ext[0] >= b and ext[1:] == (a, 1)):
         return None
     return Launch(_cdiv(b * a, 4), (b, a, t))
 
 
 def _values(shapes, consts, ext):
-    (b, a, t), (l, _b, _a, _t, d), _, (_b2, c), _ = shapes
+    (b, a, t), (l, _b, _a, _t, d), (_b2, c) = shapes[0], shapes[1], shapes[3]
     layer = consts[4]
     if a * d != c or not (0 <= layer < l) or not (ext[0] >= d and ext[1:] == (a, b)):
         return None
@@ -311,7 +311,7 @@ def _unary(shapes, consts, ext):
 
 
 def _greedy(shapes, consts, ext):
-    (b, v), _, (t, _b), _ = shapes
+    (b, v), (t, _b) = shapes[0], shapes[2]
     return Launch(b, (b, v, t)) if ext[0] >= b and ext[1:] == (1, 1) else None
 
 
@@ -320,7 +320,7 @@ def _advance(shapes, consts, ext):
 
 
 def _update(shapes, consts, ext):
-    (n,), _, _ = shapes
+    (n,) = shapes[0]
     return Launch(_elementwise(n, n), (n,)) if ext[0] >= n and ext[1:] == (1, 1) else None
 
 

@@ -1,0 +1,47 @@
+"""Decoder step on the GPU against the NumPy oracle: exact tokens/history/position, f32 state
+within atol 2e-5 / rtol 3e-4, for every run mode, storage reuse on/off and step grouping
+(benchmarks/decoder/run.py:107-197 protocol)."""
+import numpy as np
+import pytest
+
+from oracle import decoder as oracle
+from programs.decoder_config import CONFIGS, Config
+from programs.harness import DecoderSession
+
+pytestmark = pytest.mark.gpu
+
+REFERENCE_SMALL = Config(batch=1, hidden=64, heads=4, layers=2, ffn=128, vocab=256, context=8, steps=16)
+AWKWARD = Config(batch=3, hidden=48, heads=3, layers=1, ffn=80, vocab=129, context=3, steps=16)
+
+
+def run_and_check(device, c, init, steps, modes=("ordinary", "graph", "capture"), groups=(1,)):
+    initial, prompts = oracle.make_inputs(c, 123, init=init)
+    session = DecoderSession(c, device, arrays=initial)
+    references = {n: oracle.expected(initial, c, n) for n in {1, steps}}
+    worst = 0.0
+    for reuse, inv in session.invocations.items():
+        for mode in modes:
+            for group in groups:
+                if steps % group:
+                    continue
+                session.state.reset()
+                inv.run(mode=mode, batch_size=1)
+                worst = max(worst, session.state.verify(references[1]))
+                session.state.reset()
+                for _ in range(steps // group):
+                    inv.run(mode=mode, batch_size=group)
+                worst = max(worst, session.state.verify(references[steps]))
+    return worst, session
+
+
+@pytest.mark.parametrize("name", ["small", "wide", "deep"])
+def test_baseline_configs_match_oracle(device, name):
+    c = CONFIGS[name]
+    worst, _ = run_and_check(device, c, "baseline", c.steps, groups=(1, 16))
+    assert worst < 2e-5
+
+
+@pytest.mark.parametrize("config", [REFERENCE_SMALL, AWKWARD], ids=["reference_small", "awkward"])
+def test_reference_configs_match_oracle(device, config):
+    worst, _ = run_and_check(device, config, "reference", config.steps, groups=(1, 4))
+    assert worst < 2e-5
