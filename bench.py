@@ -1,0 +1,288 @@
+#!/usr/bin/env python3
+"""Decode-step benchmark of the CKL MI355X backend (one GPU).
+
+For each decoder configuration (small, wide, deep, large) the decode program is
+lowered, compiled with storage reuse off and on, bound to device-resident synthetic state,
+prefilled on the GPU (teacher-forced prompt), and timed per variant with the protocol of the
+reference harness (benchmarks/decoder/run.py:160-197): every sample resets the mutable state and
+times one 16-step generation with HIP events on the invocation stream; samples rotate and reverse
+the variant order; the median microseconds per decode step is reported.
+
+Variants (run.py:24-38): sequential/capture/inferred with reuse off and on, and the 16-step
+batched capture/inferred graphs. "inferred" executes the DAG-derived graph; "capture" is a
+single-stream capture of ordinary launches.
+
+Output: one JSON line on stdout (details per configuration under "configs"); human-readable
+progress on stderr. The CPU baseline (NumPy restatement of the reference decoder step) is timed on
+this host's cores on the same inputs and is also the checker of the measured runs' tokens.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for path in (ROOT / "composable-kernel-language_amd" / "python", ROOT / "composable-kernel-language_amd", ROOT):
+    sys.path.insert(0, str(path))
+
+import numpy as np  # noqa: E402
+
+HBM_PEAK = 8.0e12          # MI355X HBM3E bytes/s
+METRIC = "median µs/decode step: inferred hipGraph vs stream capture; scratch bytes"
+
+
+def log(*parts):
+    print(*parts, file=sys.stderr, flush=True)
+
+
+def variants(steps):
+    return [("sequential", False, "ordinary", 1), ("capture", False, "capture", 1), ("inferred", False, "graph", 1),
+            ("sequential_reuse", True, "ordinary", 1), ("capture_reuse", True, "capture", 1),
+            ("inferred_reuse", True, "graph", 1), ("batched_capture", True, "capture", steps),
+            ("batched_inferred", True, "graph", steps)]
+
+
+def algorithmic_step_bytes(c, position):
+    """HBM bytes one decode step must move at `position` (weights + KV read/write + logits +
+    embedding gather): 4*[L(4C^2+3CF) + CV + (2L+1)C + BC] + 8*L*B*A*D*(p+1) + 8*L*B*A*D + 4*B*V."""
+    b, h, l, f, v, a, d = c.batch, c.hidden, c.layers, c.ffn, c.vocab, c.heads, c.head_dim
+    weights = 4 * (l * (4 * h * h + 3 * h * f) + h * v + (2 * l + 1) * h + b * h)
+    kv_read = 8 * l * b * a * d * (position + 1)
+    kv_write = 8 * l * b * a * d
+    return weights + kv_read + kv_write + 4 * b * v
+
+
+def kernel_bytes(name, c, position):
+    """Algorithmic HBM bytes of one launch of a library kernel (for the roofline line)."""
+    b, h, f, v, a, d = c.batch, c.hidden, c.ffn, c.vocab, c.heads, c.head_dim
+    rows = position + 1
+    if name == "ckl_attention_scores":
+        return 4 * (b * a * rows * d + b * h + b * a * rows)
+    if name == "ckl_attention_values":
+        return 4 * (b * a * rows * d + b * a * rows + b * h)
+    return None
+
+
+LIGHT_RESET = ("tokens", "position", "history", "logits")
+
+
+def time_variants(session, c, samples, warmup, log_prefix):
+    """Timing resets restore the small mutable state only: every run rewrites the cache rows it
+    reads (positions >= the prefill position) before reading them, with deterministic kernels."""
+    state = session.state
+    rows = variants(c.steps)
+    metrics = {name: [] for name, *_ in rows}
+    setup = {}
+    for name, reuse, mode, group in rows:
+        inv = session.invocations[reuse]
+        state.reset(LIGHT_RESET)
+        setup[name] = inv.benchmark(iterations=1, mode=mode, batch_size=group)["graph_setup_ms"]
+        for _ in range(warmup):
+            state.reset(LIGHT_RESET)
+            inv.benchmark(iterations=c.steps // group, mode=mode, batch_size=group)
+    results = {}
+    for sample in range(samples):
+        offset = sample % len(rows)
+        order = rows[offset:] + rows[:offset]
+        if sample % 2:
+            order = list(reversed(order))
+        for name, reuse, mode, group in order:
+            inv = session.invocations[reuse]
+            state.reset(LIGHT_RESET)
+            timing = inv.benchmark(iterations=c.steps // group, mode=mode, batch_size=group)
+            metrics[name].append(timing["stream_us"])
+            results.setdefault(name, []).append(timing["wall_us"])
+    table = {}
+    for name, reuse, mode, group in rows:
+        launches = session.invocations[reuse].launch_count(mode=mode, batch_size=group)
+        table[name] = dict(median_us=statistics.median(metrics[name]), min_us=min(metrics[name]),
+                           max_us=max(metrics[name]), wall_us=statistics.median(results[name]),
+                           graph_setup_ms=setup[name], launches_per_submission=launches, steps_per_submission=group,
+                           samples=metrics[name])
+        log(f"{log_prefix} {name:18s} {table[name]['median_us']:9.2f} us/step  launches/submission={launches}")
+    return table
+
+
+def run_config(name, c, args, device):
+    from programs.harness import DecoderSession, synthetic_inputs
+    t0 = time.time()
+    arrays, prompts = synthetic_inputs(c, args.seed, init="baseline")
+    session = DecoderSession(c, device, arrays=arrays)
+    t1 = time.time()
+    session.prefill(prompts)
+    t2 = time.time()
+    log(f"[{name}] inputs+compile+bind {t1 - t0:.1f}s, device prefill of {c.context - 1} steps {t2 - t1:.2f}s")
+    table = time_variants(session, c, args.samples, args.warmup, f"[{name}]")
+    heap = {}
+    for reuse, program in session.programs.items():
+        heap[str(reuse)] = sum(int(line.split("bytes = ")[1].split(" ")[0]) for line in program.executable_ir.splitlines()
+                               if '"ckl_exec.heap"' in line)
+    # State after one timed generation (the checker compares it with the CPU oracle).
+    session.state.reset()
+    session.invocations[True].run(mode="graph", batch_size=c.steps)
+    final = {k: session.state.download(k) for k in ("tokens", "history", "position", "logits")}
+    inferred, capture = table["inferred"]["median_us"], table["capture"]["median_us"]
+    position = c.context - 1
+    mean_bytes = statistics.mean(algorithmic_step_bytes(c, position + s) for s in range(c.steps))
+    step_us = table["batched_inferred"]["median_us"]
+    result = dict(config=vars(c), steps=c.steps, variants=table,
+                  inferred_us=inferred, capture_us=capture, ordinary_us=table["sequential"]["median_us"],
+                  inferred_over_capture=capture / inferred,
+                  inferred_reuse_over_capture_reuse=table["capture_reuse"]["median_us"] / table["inferred_reuse"]["median_us"],
+                  scratch_bytes={"reuse_off": heap["False"], "reuse_on": heap["True"]},
+                  tokens_per_s=c.batch * 1e6 / step_us,
+                  algorithmic_bytes_per_step=mean_bytes,
+                  step_hbm_fraction=mean_bytes / (step_us * 1e-6) / HBM_PEAK)
+    log(f"[{name}] inferred/capture speedup {result['inferred_over_capture']:.3f}x; scratch {heap['False']} -> {heap['True']} B; "
+        f"step roofline {result['step_hbm_fraction']:.3f} of 8 TB/s")
+    return session, result, final
+
+
+def kernel_roofline(session, c, iterations=10):
+    """Time every plan node of one step with HIP events; return per-kernel averages and the
+    roofline entry of the dominant kernel (largest total time per step)."""
+    inv = session.invocations[True]
+    session.state.reset()
+    position = c.context - 1
+    per_kernel = {}
+    for index in range(inv.node_count):
+        kernel = inv.node_name(index)
+        if kernel == "ckl_advance":
+            continue
+        us = inv.time_node(index, iterations)
+        entry = per_kernel.setdefault(kernel, {"launches": 0, "total_us": 0.0, "avg_us": []})
+        entry["launches"] += 1
+        entry["total_us"] += us
+        entry["avg_us"].append(us)
+    session.state.reset()
+    dominant = max(per_kernel, key=lambda k: per_kernel[k]["total_us"])
+    avg = statistics.mean(per_kernel[dominant]["avg_us"])
+    algorithmic = kernel_bytes(dominant, c, position)
+    summary = {k: {"launches": v["launches"], "avg_us": statistics.mean(v["avg_us"]), "total_us": v["total_us"]}
+               for k, v in sorted(per_kernel.items(), key=lambda kv: -kv[1]["total_us"])}
+    roofline = None
+    if algorithmic is not None:
+        achieved = algorithmic / (avg * 1e-6)
+        roofline = {"bound": "hbm", "kernel": dominant, "achieved": achieved / 1e9, "peak": HBM_PEAK / 1e9,
+                    "unit": "GB/s", "frac": achieved / HBM_PEAK, "traffic": None,
+                    "algorithmic_bytes_per_launch": algorithmic, "avg_launch_us": avg}
+    return summary, dominant, roofline
+
+
+def cpu_baseline(session, c, final, threads=None):
+    """NumPy oracle (restatement of the reference's reference.py step) timed on this host, from the
+    same prefilled state; also checks the GPU generation's tokens and logits."""
+    from oracle import decoder as oracle
+    state = session.state
+    initial = {k: (v.copy() if k in oracle.MUTABLE else v) for k, v in state.initial.items()}
+    steps = c.steps
+    times = []
+    reference = None
+    samples = 3 if c.hidden >= 1024 else 7
+    for _ in range(samples):
+        start = time.perf_counter()
+        reference = oracle.expected(initial, c, steps)
+        times.append((time.perf_counter() - start) / steps * 1e6)
+    ok_tokens = np.array_equal(final["history"], reference["history"]) and np.array_equal(final["tokens"], reference["tokens"])
+    logits_err = float(np.max(np.abs(final["logits"] - reference["logits"]) / (np.abs(reference["logits"]) + 1e-6)))
+    close = bool(np.allclose(final["logits"], reference["logits"], atol=2e-5, rtol=3e-4))
+    return dict(value=statistics.median(times), unit="us/step", cores=threads or os.cpu_count(), kind="port",
+                sample=f"{samples} x {steps}-step NumPy generations from the GPU-prefilled state, B={c.batch}",
+                tokens_match=bool(ok_tokens), logits_allclose=close, logits_max_rel_err=logits_err)
+
+
+def vector_pipeline(device, samples):
+    import ckl
+    from programs import vector_pipeline as vp
+    n = 1048576
+    compiled = {reuse: vp.lower(n).compile(fuse_pointwise=False, reuse_storage=reuse) for reuse in (False, True)}
+    spec = ckl.BufferSpec((n,), ckl.f32)
+    src, dst = device.empty(spec), device.empty(spec)
+    x = np.random.default_rng(123).uniform(-1, 1, n).astype(np.float32)
+    src.copy_from_host(x)
+    inv = compiled[True].bind(src, dst, 0.5)
+    out = {}
+    for mode in ("ordinary", "capture", "graph"):
+        inv.run(mode=mode)
+        got = np.empty_like(x)
+        dst.copy_to_host(got)
+        assert np.array_equal(got, (x + np.float32(0.5)) + np.float32(0.5))
+        inv.benchmark(iterations=20, mode=mode)
+        out[mode] = statistics.median(inv.benchmark(iterations=100, mode=mode)["stream_us"] for _ in range(samples))
+    heap = {str(r): sum(int(l.split("bytes = ")[1].split(" ")[0]) for l in p.executable_ir.splitlines()
+                        if '"ckl_exec.heap"' in l) for r, p in compiled.items()}
+    log(f"[vector_pipeline] us/step {out}; heap {heap}")
+    return dict(us_per_step=out, heap_bytes=heap, bytes_per_step=16 * n)
+
+
+def main():
+    parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=16, help="decode steps per timed generation (config steps)")
+    parser.add_argument("--warmup", type=int, default=3)
+    parser.add_argument("--samples", type=int, default=7)
+    parser.add_argument("--seed", type=int, default=123)
+    parser.add_argument("--configs", nargs="+", default=["small", "wide", "deep", "large"])
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--output", type=Path, default=None, help="also write the full JSON result here")
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU: every box here has one MI355X; "
+                          "multi-GPU sharding is a design note (DESIGN.md), not a measured path"}))
+        sys.exit(2)
+    import dataclasses
+    import ckl
+    from programs.decoder_config import CONFIGS
+
+    device = ckl.Device()
+    log(f"device: {device.name}")
+    configs = {}
+    headline = None
+    for name in args.configs:
+        c = dataclasses.replace(CONFIGS[name], steps=args.steps)
+        session, result, final = run_config(name, c, args, device)
+        if name == "large":
+            summary, dominant, roofline = kernel_roofline(session, c)
+            result["kernels"] = summary
+            result["roofline"] = roofline
+            log(f"[large] dominant kernel {dominant}: {roofline}")
+        if not args.no_cpu_baseline and name in ("small",):
+            result["cpu_baseline"] = cpu_baseline(session, c, final)
+            log(f"[{name}] cpu baseline {result['cpu_baseline']}")
+        configs[name] = result
+        if name == "small":
+            headline = result
+        del session
+    vector = vector_pipeline(device, args.samples)
+    head = headline or next(iter(configs.values()))
+    large = configs.get("large", {})
+    line = {
+        "metric": METRIC, "value": head["inferred_us"], "unit": "us/step", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": head["inferred_us"] / 1000.0, "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic (seeded N(0,0.02) weights, random prompts)",
+        "config": {"workload": "small decoder (B8 C64 A4x16 L2 F256 V256, ctx 16, 16 greedy steps)",
+                   "inferred_us": head["inferred_us"], "capture_us": head["capture_us"],
+                   "ordinary_us": head["ordinary_us"], "inferred_over_capture": head["inferred_over_capture"],
+                   "scratch_bytes": head["scratch_bytes"], "tokens_per_s": head["tokens_per_s"]},
+        "roofline": large.get("roofline"),
+        "cpu_baseline": head.get("cpu_baseline"),
+        "configs": {k: {kk: vv for kk, vv in v.items() if kk not in ("variants", "kernels")} |
+                    {"variants": {vn: {"median_us": vv["median_us"], "launches": vv["launches_per_submission"]}
+                                  for vn, vv in v["variants"].items()}} for k, v in configs.items()},
+        "vector_pipeline": vector,
+        "host": {"cpu": platform.processor() or platform.machine(), "nproc": os.cpu_count(), "numpy": np.__version__},
+    }
+    if args.output:
+        full = dict(line, configs_full=configs)
+        args.output.write_text(json.dumps(full, indent=1, default=float) + "\n")
+    print(json.dumps(line, default=float))
+
+
+if __name__ == "__main__":
+    main()

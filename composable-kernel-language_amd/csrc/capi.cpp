@@ -319,6 +319,22 @@ int ckl_invocation_launch_count(ckl_invocation *invocation, int mode, uint64_t b
   });
 }
 
+int ckl_invocation_time_node(ckl_invocation *invocation, uint64_t index, uint64_t iterations, double *average_us) {
+  return guarded([&] {
+    require(invocation, "invocation");
+    require(average_us, "average_us");
+    *average_us = invocation->invocation->timeNode(index, iterations);
+  });
+}
+
+const char *ckl_invocation_node_name(ckl_invocation *invocation, uint64_t index) {
+  try {
+    return invocation ? invocation->invocation->nodeName(index).c_str() : "";
+  } catch (...) {
+    return "";
+  }
+}
+
 void ckl_invocation_release(ckl_invocation *invocation) { delete invocation; }
 
 } // extern "C"

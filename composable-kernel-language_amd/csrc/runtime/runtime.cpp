@@ -390,6 +390,32 @@ std::array<double, 3> Invocation::benchmark(int mode, uint64_t iterations, uint6
   return result;
 }
 
+double Invocation::timeNode(size_t index, uint64_t iterations) {
+  if (!iterations) throw std::invalid_argument("iterations must be positive");
+  std::lock_guard<std::mutex> lock(runMutex);
+  const Launch &launch = plan.nodes.at(index).launch;
+  device->makeCurrent();
+  check(hipStreamSynchronize(stream), "hipStreamSynchronize");
+  hipEvent_t start = nullptr, stop = nullptr;
+  check(hipEventCreate(&start), "hipEventCreate");
+  float elapsed = 0;
+  try {
+    check(hipEventCreate(&stop), "hipEventCreate");
+    check(hipEventRecord(start, stream), "hipEventRecord");
+    for (uint64_t k = 0; k < iterations; ++k) launchOne(launch, stream);
+    check(hipEventRecord(stop, stream), "hipEventRecord");
+    check(hipEventSynchronize(stop), "hipEventSynchronize");
+    check(hipEventElapsedTime(&elapsed, start, stop), "hipEventElapsedTime");
+  } catch (...) {
+    hipEventDestroy(start);
+    if (stop) hipEventDestroy(stop);
+    throw;
+  }
+  hipEventDestroy(start);
+  hipEventDestroy(stop);
+  return double(elapsed) * 1000.0 / double(iterations);
+}
+
 // ====================================================================== callbacks
 // The callback protocol of lib/Runtime/NvidiaProgram.cpp:48-108: exceptions never unwind
 // through the entry; the first failure is recorded and later callbacks become no-ops.

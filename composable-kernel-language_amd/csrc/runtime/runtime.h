@@ -108,6 +108,10 @@ struct Invocation {
   std::array<double, 3> benchmark(int mode, uint64_t iterations, uint64_t batch);
   size_t nodeCount() const { return plan.nodes.size(); }
   size_t graphNodeCount(int mode, uint64_t batch);
+  // Average duration (us) of plan node `index` launched `iterations` times back to back on the
+  // invocation stream, bracketed by HIP events.
+  double timeNode(size_t index, uint64_t iterations);
+  const std::string &nodeName(size_t index) const { return plan.nodes.at(index).launch.name; }
 
 private:
   void validate(int mode, uint64_t batch) const;

@@ -304,6 +304,17 @@ class Invocation(_ContextManager):
             self._native_resource.pointer, self._execution(False, mode, batch_size), batch_size, ctypes.byref(count)))
         return int(count.value)
 
+    def node_name(self, index: int) -> str:
+        return _native.native().ckl_invocation_node_name(self._native_resource.pointer, index).decode()
+
+    def time_node(self, index: int, iterations: int = 20) -> float:
+        """Average microseconds of plan node `index` launched `iterations` times back to back
+        (HIP events on the invocation stream). The node's writes are repeated."""
+        out = ctypes.c_double()
+        _native.check(_native.native().ckl_invocation_time_node(self._native_resource.pointer, index, iterations,
+                                                                ctypes.byref(out)))
+        return out.value
+
     def benchmark(self, *, iterations=200, graph=False, mode=None, batch_size=1) -> dict:
         """Time `iterations` submissions of `batch_size` program executions with HIP events on
         the invocation stream; returns per-program stream and wall microseconds plus graph setup."""

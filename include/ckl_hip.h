@@ -113,6 +113,13 @@ int ckl_invocation_benchmark(ckl_invocation *invocation, int mode, uint64_t iter
 uint64_t ckl_invocation_node_count(ckl_invocation *invocation);
 /* Number of device launches (graph nodes) one execution of `batch` steps submits in `mode`. */
 int ckl_invocation_launch_count(ckl_invocation *invocation, int mode, uint64_t batch, uint64_t *count);
+/* Kernel-level timing for roofline measurement (no reference counterpart; the reference profiles
+ * with nsys): plan node `index` (0 .. node_count-1, executable-plan order) is launched
+ * `iterations` times back to back on the invocation stream between two HIP events; the average
+ * duration in microseconds is returned. The node's effects are applied `iterations` times. */
+int ckl_invocation_time_node(ckl_invocation *invocation, uint64_t index, uint64_t iterations, double *average_us);
+/* Device entry point name of plan node `index` ("" when out of range). */
+const char *ckl_invocation_node_name(ckl_invocation *invocation, uint64_t index);
 void ckl_invocation_release(ckl_invocation *invocation);
 
 /* ---------------------------------------------------------------- host-entry callbacks
