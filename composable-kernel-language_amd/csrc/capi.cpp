@@ -209,6 +209,42 @@ int ckl_opt(const char *ir, const char *passes, char **out) {
   });
 }
 
+int ckl_plan_storage(size_t nodeCount, const uint64_t *edges, size_t edgeCount, const ckl_storage_resource *resources,
+                     size_t resourceCount, int reuseStorage, uint64_t *baseline, uint64_t *planned,
+                     ckl_storage_assignment *out) {
+  return guarded([&] {
+    if (edgeCount && !edges) throw std::invalid_argument("edges must not be null");
+    if (resourceCount && (!resources || !out)) throw std::invalid_argument("resources and out must not be null");
+    std::vector<ckl::planning::GraphEdge> graph;
+    for (size_t k = 0; k < edgeCount; ++k) graph.push_back({edges[2 * k], edges[2 * k + 1]});
+    std::vector<ckl::planning::Resource> list;
+    for (size_t k = 0; k < resourceCount; ++k) {
+      const ckl_storage_resource &r = resources[k];
+      ckl::planning::Resource res;
+      res.name = "r" + std::to_string(k);
+      res.bytes = r.bytes;
+      res.alignment = r.alignment;
+      res.device = r.device;
+      res.addressSpace = r.address_space ? r.address_space : "global";
+      if (r.kind < 0 || r.kind > 2) throw std::invalid_argument("resource kind must be 0, 1 or 2");
+      res.kind = r.kind == 0 ? ckl::planning::ResourceKind::Temporary
+                 : r.kind == 1 ? ckl::planning::ResourceKind::Persistent
+                               : ckl::planning::ResourceKind::External;
+      if (r.user_count && !r.users) throw std::invalid_argument("users must not be null");
+      res.users.assign(r.users, r.users + r.user_count);
+      list.push_back(std::move(res));
+    }
+    auto plan = ckl::planning::MemoryPlanner(reuseStorage != 0).plan(nodeCount, graph, list);
+    if (baseline) *baseline = plan.baselineBytes;
+    if (planned) *planned = plan.plannedBytes;
+    const uint64_t none = ~uint64_t(0);
+    for (size_t k = 0; k < resourceCount; ++k) out[k] = {none, none, none, none};
+    for (const auto &a : plan.assignments) out[a.resource] = {a.heap, a.offset, a.slot, none};
+    for (const auto &d : plan.decisions)
+      if (!d.sharesWith.empty()) out[d.resource].shares_first = d.sharesWith.front();
+  });
+}
+
 const char *ckl_library_identity(void) { return libraryArtifact().identity.c_str(); }
 
 int ckl_device_count(void) { return ckl::rt::deviceCount(); }

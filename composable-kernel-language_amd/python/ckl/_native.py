@@ -26,6 +26,16 @@ class Argument(ctypes.Structure):
     _fields_ = [("kind", ctypes.c_int), ("buffer", ctypes.c_void_p), ("integer", ctypes.c_int64), ("real", ctypes.c_double)]
 
 
+class StorageResource(ctypes.Structure):
+    _fields_ = [("bytes", ctypes.c_uint64), ("alignment", ctypes.c_uint64), ("device", ctypes.c_int), ("kind", ctypes.c_int),
+                ("address_space", ctypes.c_char_p), ("users", ctypes.POINTER(ctypes.c_uint64)), ("user_count", ctypes.c_size_t)]
+
+
+class StorageAssignment(ctypes.Structure):
+    _fields_ = [("heap", ctypes.c_uint64), ("offset", ctypes.c_uint64), ("slot", ctypes.c_uint64),
+                ("shares_first", ctypes.c_uint64)]
+
+
 ENTRY = ctypes.CFUNCTYPE(None, ctypes.POINTER(ctypes.c_void_p))
 
 _SIGNATURES = {
@@ -41,6 +51,9 @@ _SIGNATURES = {
                                 ctypes.c_size_t, ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p)], ctypes.c_int),
     "ckl_program_release": ([ctypes.c_void_p], None),
     "ckl_opt": ([ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(ctypes.c_void_p)], ctypes.c_int),
+    "ckl_plan_storage": ([ctypes.c_size_t, ctypes.POINTER(ctypes.c_uint64), ctypes.c_size_t, ctypes.POINTER(StorageResource),
+                          ctypes.c_size_t, ctypes.c_int, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64),
+                          ctypes.POINTER(StorageAssignment)], ctypes.c_int),
     "ckl_library_identity": ([], ctypes.c_char_p),
     "ckl_device_count": ([], ctypes.c_int),
     "ckl_device_open": ([ctypes.c_int, ctypes.POINTER(ctypes.c_void_p)], ctypes.c_int),
@@ -125,6 +138,34 @@ def native_opt(ir: str, passes) -> str:
         return ctypes.string_at(out.value).decode()
     finally:
         lib.ckl_string_free(out)
+
+
+NONE = (1 << 64) - 1
+
+
+def plan_storage(node_count, edges, resources, reuse=True):
+    """Run the native storage planner. `resources`: dicts with bytes, alignment, kind
+    ("temporary" | "persistent" | "external"), users, optional device and address_space.
+    Returns (baseline_bytes, planned_bytes, [assignment dict or None per resource])."""
+    kinds = {"temporary": 0, "persistent": 1, "external": 2}
+    flat = (ctypes.c_uint64 * max(1, 2 * len(edges)))(*[v for e in edges for v in e])
+    keep = []
+    table = (StorageResource * max(1, len(resources)))()
+    for k, r in enumerate(resources):
+        users = (ctypes.c_uint64 * max(1, len(r["users"])))(*r["users"])
+        keep.append(users)
+        table[k] = StorageResource(r["bytes"], r.get("alignment", 256), r.get("device", 0), kinds[r.get("kind", "temporary")],
+                                   r.get("address_space", "global").encode(), users, len(r["users"]))
+    out = (StorageAssignment * max(1, len(resources)))()
+    baseline, planned = ctypes.c_uint64(), ctypes.c_uint64()
+    check(native().ckl_plan_storage(node_count, flat, len(edges), table, len(resources), int(reuse),
+                                    ctypes.byref(baseline), ctypes.byref(planned), out))
+    result = []
+    for k in range(len(resources)):
+        a = out[k]
+        result.append(None if a.heap == NONE else dict(heap=a.heap, offset=a.offset, slot=a.slot,
+                                                       shares_first=None if a.shares_first == NONE else a.shares_first))
+    return baseline.value, planned.value, result
 
 
 def library_identity() -> str:

@@ -70,6 +70,30 @@ void ckl_program_release(ckl_program *program);
  * comma-free list separated by ';', e.g. "build-graph;lower-graph-to-exec". */
 int ckl_opt(const char *ir, const char *passes, char **out);
 
+/* Storage planner (MemoryPlanner::plan, lib/Core/MemoryPlanner.cpp:98-204 and
+ * include/ckl/Core/MemoryPlanner.h:18-92) over an explicit graph: `edges` holds edge_count
+ * (from, to) pairs. Resource kind: 0 temporary, 1 persistent, 2 external. For each resource k,
+ * out[k] receives its heap, offset and slot (heap = UINT64_MAX for externals) and
+ * shares_first the first earlier resident of its slot (UINT64_MAX when none). */
+typedef struct {
+  uint64_t bytes;
+  uint64_t alignment;
+  int device;
+  int kind;
+  const char *address_space;
+  const uint64_t *users;
+  size_t user_count;
+} ckl_storage_resource;
+typedef struct {
+  uint64_t heap;
+  uint64_t offset;
+  uint64_t slot;
+  uint64_t shares_first;
+} ckl_storage_assignment;
+int ckl_plan_storage(size_t node_count, const uint64_t *edges, size_t edge_count, const ckl_storage_resource *resources,
+                     size_t resource_count, int reuse_storage, uint64_t *baseline_bytes, uint64_t *planned_bytes,
+                     ckl_storage_assignment *out);
+
 /* Identity of the hand-written gfx950 kernel library code object ("" when absent). */
 const char *ckl_library_identity(void);
 
