@@ -58,15 +58,30 @@ def algorithmic_step_bytes(c, position):
     return weights + kv_read + kv_write + 4 * b * v
 
 
-def kernel_bytes(name, c, position):
-    """Algorithmic HBM bytes of one launch of a library kernel (for the roofline line)."""
+def decoder_node_bytes(c, position):
+    """Algorithmic HBM bytes of every dispatch of one decode step at `position`, in plan order
+    (the order of the decode program's launches): each kernel's compulsory reads and writes."""
     b, h, f, v, a, d = c.batch, c.hidden, c.ffn, c.vocab, c.heads, c.head_dim
-    rows = position + 1
-    if name == "ckl_attention_scores":
-        return 4 * (b * a * rows * d + b * h + b * a * rows)
-    if name == "ckl_attention_values":
-        return 4 * (b * a * rows * d + b * a * rows + b * h)
-    return None
+    rows, r = position + 1, d // 2
+    hidden = 4 * b * h
+
+    def linear(i, o):
+        return ("linear", 4 * (b * i + i * o + b * o))
+
+    nodes = [("embedding", 2 * hidden + 4 * b)]
+    for _ in range(c.layers):
+        nodes += [("rms_stats", hidden + 4 * b), ("rms_apply", 2 * hidden + 4 * h + 4 * b),
+                  linear(h, h), linear(h, h), linear(h, h),
+                  ("rope", 2 * hidden + 8 * r), ("rope", 2 * hidden + 8 * r), ("append_kv", 4 * hidden),
+                  ("attention_scores", hidden + 4 * b * a * rows * d + 4 * b * a * rows),
+                  ("softmax", 8 * b * a * rows),
+                  ("attention_values", 4 * b * a * rows + 4 * b * a * rows * d + hidden),
+                  linear(h, h), ("add", 3 * hidden), ("rms_stats", hidden + 4 * b),
+                  ("rms_apply", 2 * hidden + 4 * h + 4 * b), linear(h, f), linear(h, f),
+                  ("silu", 8 * b * f), ("multiply", 12 * b * f), linear(f, h), ("add", 3 * hidden)]
+    nodes += [("rms_stats", hidden + 4 * b), ("rms_apply", 2 * hidden + 4 * h + 4 * b), linear(h, v),
+              ("greedy", 4 * b * v + 8 * b), ("advance", 8)]
+    return nodes
 
 
 LIGHT_RESET = ("tokens", "position", "history", "logits")
@@ -115,7 +130,7 @@ def run_config(name, c, args, device):
     arrays, prompts = synthetic_inputs(c, args.seed, init="baseline")
     session = DecoderSession(c, device, arrays=arrays)
     t1 = time.time()
-    session.prefill(prompts)
+    session.prefill(prompts, progress=lambda done, total: log(f"[{name}] prefill {done}/{total}"))
     t2 = time.time()
     log(f"[{name}] inputs+compile+bind {t1 - t0:.1f}s, device prefill of {c.context - 1} steps {t2 - t1:.2f}s")
     table = time_variants(session, c, args.samples, args.warmup, f"[{name}]")
@@ -145,33 +160,42 @@ def run_config(name, c, args, device):
 
 
 def kernel_roofline(session, c, iterations=10):
-    """Time every plan node of one step with HIP events; return per-kernel averages and the
-    roofline entry of the dominant kernel (largest total time per step)."""
+    """Time every plan node of one step with HIP events (back-to-back launches of the node on the
+    invocation stream) and return per-family totals and the roofline entry of the dominant family
+    (largest total time per step): algorithmic bytes per launch / average launch duration."""
     inv = session.invocations[True]
     session.state.reset()
     position = c.context - 1
+    nodes = decoder_node_bytes(c, position)
+    if len(nodes) != inv.node_count:
+        raise AssertionError("plan does not have the decode program's dispatch count")
     per_kernel = {}
-    for index in range(inv.node_count):
+    for index, (family, algorithmic) in enumerate(nodes):
         kernel = inv.node_name(index)
-        if kernel == "ckl_advance":
+        if not kernel.startswith("ckl_" + family):
+            raise AssertionError(f"plan node {index} is {kernel}, expected the {family} family")
+        if family == "advance":
             continue
         us = inv.time_node(index, iterations)
-        entry = per_kernel.setdefault(kernel, {"launches": 0, "total_us": 0.0, "avg_us": []})
+        entry = per_kernel.setdefault(family, {"launches": 0, "total_us": 0.0, "bytes": 0, "entries": set()})
         entry["launches"] += 1
         entry["total_us"] += us
-        entry["avg_us"].append(us)
+        entry["bytes"] += algorithmic
+        entry["entries"].add(kernel)
     session.state.reset()
-    dominant = max(per_kernel, key=lambda k: per_kernel[k]["total_us"])
-    avg = statistics.mean(per_kernel[dominant]["avg_us"])
-    algorithmic = kernel_bytes(dominant, c, position)
-    summary = {k: {"launches": v["launches"], "avg_us": statistics.mean(v["avg_us"]), "total_us": v["total_us"]}
+    summary = {k: {"launches": v["launches"], "avg_us": v["total_us"] / v["launches"], "total_us": v["total_us"],
+                   "algorithmic_bytes": v["bytes"], "achieved_GBps": v["bytes"] / v["total_us"] / 1e3,
+                   "entry_points": sorted(v["entries"])}
                for k, v in sorted(per_kernel.items(), key=lambda kv: -kv[1]["total_us"])}
-    roofline = None
-    if algorithmic is not None:
-        achieved = algorithmic / (avg * 1e-6)
-        roofline = {"bound": "hbm", "kernel": dominant, "achieved": achieved / 1e9, "peak": HBM_PEAK / 1e9,
-                    "unit": "GB/s", "frac": achieved / HBM_PEAK, "traffic": None,
-                    "algorithmic_bytes_per_launch": algorithmic, "avg_launch_us": avg}
+    dominant = next(iter(summary))
+    entry = summary[dominant]
+    avg = entry["avg_us"]
+    per_launch = entry["algorithmic_bytes"] / entry["launches"]
+    achieved = per_launch / (avg * 1e-6)
+    roofline = {"bound": "hbm", "kernel": f"ckl_{dominant}", "achieved": achieved / 1e9, "peak": HBM_PEAK / 1e9,
+                "unit": "GB/s", "frac": achieved / HBM_PEAK, "traffic": None,
+                "algorithmic_bytes_per_launch": per_launch, "avg_launch_us": avg,
+                "config": "large", "position": position}
     return summary, dominant, roofline
 
 
@@ -251,6 +275,9 @@ def main():
             summary, dominant, roofline = kernel_roofline(session, c)
             result["kernels"] = summary
             result["roofline"] = roofline
+            for family, row in summary.items():
+                log(f"[large] {family:18s} launches={row['launches']:3d} avg={row['avg_us']:9.2f} us "
+                    f"total={row['total_us']:9.2f} us  {row['achieved_GBps']:8.1f} GB/s")
             log(f"[large] dominant kernel {dominant}: {roofline}")
         if not args.no_cpu_baseline and name in ("small",):
             result["cpu_baseline"] = cpu_baseline(session, c, final)

@@ -809,6 +809,7 @@ std::string ExecPlan::print() const {
         {"logical_block", Attr::denseI64(k.logicalBlock)}, {"logical_grid", Attr::denseI64(k.logicalGrid)},
         {"shared_memory", Attr::integer(k.sharedMemory)}};
     if (!k.group.empty()) e.push_back({"group", Attr::string(k.group)});
+    if (k.workspace) e.push_back({"workspace", Attr::integer(k.workspace)});
     out << "    \"ckl_exec.kernel\"() <" << Attr::dictOf(e).str() << "> : () -> ()\n";
   }
   out << "  }) : () -> ()\n";
@@ -969,6 +970,7 @@ ExecPlan lowerGraphToExec(const Module &module, const Op *function, const Graph 
     k.block = op->attr("ckl.hip.block") ? dims3(op->attr("ckl.hip.block")) : k.logicalBlock;
     if (const Attr *shared = op->attr("ckl.hip.shared_memory")) k.sharedMemory = shared->i;
     if (const Attr *group = op->attr("ckl.hip.group")) k.group = group->s;
+    if (const Attr *workspace = op->attr("ckl.hip.workspace")) k.workspace = workspace->i;
 
     std::vector<Value *> actuals = dispatchArguments(op);
     for (size_t slot = 0; slot < actuals.size(); ++slot) {
@@ -1115,7 +1117,7 @@ std::string prepareHip(Module &module, const PrepareOptions &options) {
       dispatch->attrs["artifact"] = *art;
       dispatch->attrs["implementation"] = *impl;
       dispatch->attrs["ckl.hip.entry_point"] = *entry;
-      for (const char *key : {"grid", "block", "shared_memory", "constants", "group"})
+      for (const char *key : {"grid", "block", "shared_memory", "constants", "group", "workspace"})
         if (const Attr *a = chosen->get(key)) dispatch->attrs[std::string("ckl.hip.") + key] = *a;
     } else {
       dispatch->attrs["artifact"] = Attr::string(artifact);

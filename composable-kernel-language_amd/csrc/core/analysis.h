@@ -144,6 +144,7 @@ struct ExecKernel {
   std::vector<int64_t> logicalGrid, logicalBlock;
   int64_t sharedMemory = 0;
   std::string group;                  // sibling-grouping family ("" = none)
+  int64_t workspace = 0;              // private device workspace bytes of a library kernel
   std::vector<ExecArgument> arguments;
   std::vector<int64_t> dependencies;
 };

@@ -42,6 +42,7 @@ struct Sink {
   virtual void kernel(const ExecKernel &k) = 0;
   virtual void argumentResource(uint64_t id, uint64_t offset) = 0;
   virtual void argumentValue(const void *bytes, uint64_t size, const std::string &what) = 0;
+  virtual void workspace(uint64_t bytes) = 0;
   virtual void dependency(uint64_t id) = 0;
   virtual void commit(uint64_t id) = 0;
 };
@@ -87,6 +88,8 @@ void walkEntry(const CompiledProgram &program, Sink &sink, void **values) {
         sink.argumentValue(a->bytes.data(), a->bytes.size(), "");
       }
     }
+    if (k.workspace < 0) throw CompileError("library workspace size must be non-negative");
+    if (k.workspace) sink.workspace(uint64_t(k.workspace));
     for (int64_t d : k.dependencies) sink.dependency(uint64_t(d));
     sink.commit(uint64_t(k.id));
   }
@@ -107,6 +110,7 @@ struct CallbackSink : Sink {
   }
   void argumentResource(uint64_t id, uint64_t offset) override { ckl_argument_resource(frame, id, offset); }
   void argumentValue(const void *bytes, uint64_t size, const std::string &) override { ckl_argument_value(frame, bytes, size); }
+  void workspace(uint64_t bytes) override { ckl_workspace(frame, bytes); }
   void dependency(uint64_t id) override { ckl_dependency(frame, id); }
   void commit(uint64_t id) override { ckl_commit(frame, id); }
 };
@@ -132,6 +136,7 @@ struct TextSink : Sink {
     if (!what.empty()) out << "ckl_argument_value(" << what << ", " << size << ")\n";
     else out << "ckl_argument_value([" << hexBytes(bytes, size) << "], " << size << ")\n";
   }
+  void workspace(uint64_t bytes) override { out << "ckl_workspace(" << bytes << ")\n"; }
   void dependency(uint64_t id) override { out << "ckl_dependency(" << id << ")\n"; }
   void commit(uint64_t id) override { out << "ckl_commit(" << id << ")\n"; }
 };

@@ -26,13 +26,16 @@ template <typename Args> struct CKL_ALIGN Group {
   int count;
 };
 
-#define CKL_ENTRY(name, Args, body)                                                                  \
-  extern "C" __global__ __launch_bounds__(kBlock) void ckl_##name(const Args a) { body(a, blockIdx.x); } \
-  extern "C" __global__ __launch_bounds__(kBlock) void ckl_##name##_group(const Group<Args> g) {      \
+#define CKL_ENTRY_ATTR(name, Args, body, attributes)                                                 \
+  extern "C" __global__ __launch_bounds__(kBlock) attributes void ckl_##name(const Args a) { body(a, blockIdx.x); } \
+  extern "C" __global__ __launch_bounds__(kBlock) attributes void ckl_##name##_group(const Group<Args> g) { \
     int b = blockIdx.x, m = 0;                                                                        \
     while (m + 1 < g.count && b >= g.start[m + 1]) ++m;                                               \
     body(g.m[m], b - g.start[m]);                                                                     \
   }
+#define CKL_ENTRY(name, Args, body) CKL_ENTRY_ATTR(name, Args, body, )
+// Streaming kernels that keep several loads in flight per lane trade occupancy for registers.
+#define CKL_TWO_WAVES __attribute__((amdgpu_waves_per_eu(1, 2)))
 
 // ------------------------------------------------------------------ wave64 reductions (DPP)
 template <int Ctrl> __device__ __forceinline__ float dpp(float v) {
@@ -164,51 +167,302 @@ CKL_ENTRY(rms_apply, RmsApplyArgs, rms_apply_body)
 
 // ------------------------------------------------------------------ linear
 // dst[b, o] = sum_i x[b, i] * w[layer, i, o]   (workloads.py:61-69)
-// 64 output columns per block (one per lane); the 4 waves split the reduction range; x is
-// staged through LDS in chunks and broadcast; the 4 partial sums are combined through LDS in a
-// fixed order. Rows are processed in tiles of kRows.
-struct CKL_ALIGN LinearArgs { const float *x; const float *w; float *dst; int B, I, O, layer; };
-constexpr int kRows = 8;
-constexpr int kChunk = 128;
-__device__ void linear_body(const LinearArgs &a, int block) {
-  __shared__ float xs[kRows][kChunk];
-  __shared__ float partial[4][kRows][64];
-  int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  int o = block * 64 + lane;
-  const float *w = a.w + long(a.layer) * a.I * a.O;
-  for (int r0 = 0; r0 < a.B; r0 += kRows) {
-    float acc[kRows];
-#pragma unroll
-    for (int r = 0; r < kRows; ++r) acc[r] = 0.f;
-    for (int k0 = 0; k0 < a.I; k0 += kChunk) {
-      __syncthreads();
-      for (int e = threadIdx.x; e < kRows * kChunk; e += kBlock) {
-        int r = e / kChunk, k = e % kChunk;
-        xs[r][k] = (r0 + r < a.B && k0 + k < a.I) ? a.x[long(r0 + r) * a.I + k0 + k] : 0.f;
-      }
-      __syncthreads();
-      int kEnd = min(kChunk, a.I - k0);
-      if (o < a.O) {
-        for (int k = wave; k < kEnd; k += 4) {
-          float wv = w[long(k0 + k) * a.O + o];
-#pragma unroll
-          for (int r = 0; r < kRows; ++r) acc[r] += xs[r][k] * wv;
-        }
-      }
+//
+// The weight matrix is streamed from HBM exactly once per launch. The grid is
+// rowTiles x kSplit x tilesN workgroups of 256 threads (4 waves): workgroup (rt, kg, tn) owns
+// output tile tn (a column range) for batch-row tile rt over the reduction slice
+// [kg*kChunk, (kg+1)*kChunk), which its 4 waves share.
+//   ckl_linear (vector, B <= 16): lane <-> output column (64 per tile), rows accumulated in
+//           VGPRs, x staged through LDS;
+//   ckl_linear_mfma1/4 (f32 MFMA, B > 16): v_mfma_f32_32x32x2f32 over 32 batch rows; each lane loads
+//           J = 1 / 4 consecutive weight columns with one vector load, and MFMA j accumulates
+//           columns {J*c + j}, so one wave owns a 32 x 32J tile. The K index is permuted so the
+//           A operand (x) is one float4 load per 8 reduction rows.
+// Partial tiles of the 4 waves are added through LDS in wave order. With kSplit > 1 every
+// workgroup writes its partial tile to the workspace with agent-coherent stores and bumps the
+// tile's completion counter; the last one to arrive adds the kSplit partials in kg order,
+// writes dst and resets the counter, so the result is deterministic and replays need no reset.
+//
+// workspace layout: counters (rowTiles*tilesN uint32, padded to 256 B), then partial tiles
+// float[kSplit][rowTiles*rowsPerTile][O] (rowsPerTile = 32 for MFMA, B for the vector path).
+struct CKL_ALIGN LinearArgs {
+  const float *x; const float *w; float *dst; int B, I, O, layer;
+  int tilesN, kSplit, kChunk, pad;
+  unsigned char *workspace;
+};
+constexpr int kVectorRows = 16;
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+// s_waitcnt immediate (gfx9 encoding) that waits for vmcnt == 0 only: outstanding vector memory
+// operations of the wave, stores included, have completed.
+constexpr int kWaitStores = 0x0F70;
+
+__device__ __forceinline__ int counter_bytes(int count) { return (count * 4 + 255) & ~255; }
+
+// Cross-workgroup partial tiles live in the workspace and are written and read only with
+// agent-scope atomic stores/loads (sc1: coherent across the MI355X's per-XCD L2 caches without
+// the whole-L2 writeback/invalidate an agent-scope fence costs).
+__device__ __forceinline__ void partial_store(float *p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float partial_load(const float *p) {
+  return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Returns true in every thread of the last workgroup to finish a split tile. Only wave 0 of a
+// workgroup writes its partial tile; it waits until those agent-coherent stores have completed
+// (s_waitcnt vmcnt(0)) before bumping the tile's completion counter, so the workgroup that
+// observes the final count reads every partial through the same coherent path.
+__device__ __forceinline__ bool split_arrive(unsigned *counter, int parts, int wave) {
+  __shared__ int last;
+  if (wave == 0) {
+    __builtin_amdgcn_s_waitcnt(kWaitStores);
+    if (threadIdx.x == 0) {
+      unsigned previous = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      int isLast = previous == unsigned(parts - 1);
+      if (isLast) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      last = isLast;
     }
-#pragma unroll
-    for (int r = 0; r < kRows; ++r) partial[wave][r][lane] = acc[r];
-    __syncthreads();
-    for (int e = threadIdx.x; e < kRows * 64; e += kBlock) {
-      int r = e / 64, c = e % 64;
-      int oo = block * 64 + c;
-      if (r0 + r < a.B && oo < a.O)
-        a.dst[long(r0 + r) * a.O + oo] = ((partial[0][r][c] + partial[1][r][c]) + partial[2][r][c]) + partial[3][r][c];
-    }
-    __syncthreads();
+  }
+  __syncthreads();
+  return last;
+}
+
+// Adds the kSplit partial tiles (rows [r0, r0+rows), columns [c0, c0+cols)) in split order
+// and writes dst.
+__device__ void split_finish(const LinearArgs &a, const float *partial, long planeStride, int r0, int rows, int c0,
+                             int cols) {
+  for (int e = threadIdx.x; e < rows * cols; e += kBlock) {
+    int r = r0 + e / cols, c = c0 + e % cols;
+    if (r >= a.B || c >= a.O) continue;
+    float total = 0.f;
+    for (int g = 0; g < a.kSplit; ++g) total += partial_load(partial + g * planeStride + long(r) * a.O + c);
+    a.dst[long(r) * a.O + c] = total;
   }
 }
+
+template <int J> __device__ __forceinline__ void load_columns(float (&out)[J], const float *p) {
+  if constexpr (J == 4) {
+    float4 v = *reinterpret_cast<const float4 *>(p);
+    out[0] = v.x; out[1] = v.y; out[2] = v.z; out[3] = v.w;
+  } else if constexpr (J == 2) {
+    float2 v = *reinterpret_cast<const float2 *>(p);
+    out[0] = v.x; out[1] = v.y;
+  } else {
+    out[0] = *p;
+  }
+}
+
+// 16 reduction rows of one lane (two 8-row super-steps): x[row][k+8u .. k+8u+3] and the lane's
+// J weight columns of rows k+8u+i. Full stages load without predicates or selects, so the next
+// stage's loads stay in flight under the current stage's MFMAs: a batch row >= B (x row clamped
+// to 0) only feeds output row >= B and a column >= O (clamped to column 0) only feeds output
+// column >= O, neither of which is stored. The tail stage zeroes reduction rows past k1 (their
+// addresses are clamped to row k1-1).
+template <int J> struct MfmaStage {
+  float x[2][4];
+  float w[2][4][J];
+};
+
+template <int J, bool Tail>
+__device__ __forceinline__ void mfma_load(MfmaStage<J> &st, const float *xr, const float *w, long O, int k, int k1) {
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int kk = k + 8 * u;
+    if constexpr (!Tail) {
+      float4 v = *reinterpret_cast<const float4 *>(xr + kk);
+      st.x[u][0] = v.x; st.x[u][1] = v.y; st.x[u][2] = v.z; st.x[u][3] = v.w;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (Tail) {
+        const bool inside = kk + i < k1;
+        const int kr = min(kk + i, k1 - 1);
+        st.x[u][i] = inside ? xr[kr] : 0.f;
+        float c[J];
+        load_columns<J>(c, w + long(kr) * O);
+#pragma unroll
+        for (int j = 0; j < J; ++j) st.w[u][i][j] = inside ? c[j] : 0.f;
+      } else {
+        load_columns<J>(st.w[u][i], w + long(kk + i) * O);
+      }
+    }
+  }
+}
+
+template <int J> __device__ __forceinline__ void mfma_compute(const MfmaStage<J> &st, floatx16 (&acc)[J]) {
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < J; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(st.x[u][i], st.w[u][i][j], acc[j], 0, 0, 0);
+}
+
+template <int J> __device__ void linear_mfma(const LinearArgs &a, int block, float *smem) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform: scalar loop control
+  const int m = lane & 31, s = lane >> 5;
+  const int tn = block % a.tilesN, rest = block / a.tilesN;
+  const int kg = rest % a.kSplit, rt = rest / a.kSplit;
+  const int n = tn * 32 * J + J * m;               // first of this lane's J columns
+  const bool colOk = n < a.O;                      // host guarantees O % J == 0
+  const int row = rt * 32 + m;
+  const bool rowOk = row < a.B;
+  const float *xr = a.x + long(rowOk ? row : 0) * a.I;
+  const float *w = a.w + long(a.layer) * a.I * a.O + (colOk ? n : 0);
+  const int kb0 = min(kg * a.kChunk, a.I), kb1 = min(kb0 + a.kChunk, a.I);
+
+  floatx16 acc[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[j][r] = 0.f;
+
+  // The slice is cut into 16-row stages dealt round-robin to the 4 waves (wave w takes stages
+  // w, w+4, ...), so the waves of a workgroup stream neighbouring weight rows at any moment.
+  // Full stages are double-buffered: stage u+1's loads are in flight while stage u feeds the
+  // MFMAs. The loop body has no conditional loads (the compiler would sink them into the
+  // condition and drain the load queue at the join); with an even stage count the last prefetch
+  // re-reads the last stage, an L2 hit. sched_barrier keeps each stage's loads issued as one
+  // group ahead of the other stage's MFMAs. A ragged last stage is handled by its owner.
+  const int fullTotal = (kb1 - kb0) / 16;
+  const int full = fullTotal > wave ? (fullTotal - wave + 3) / 4 : 0;
+  const int k = kb0 + 16 * wave + 4 * s;               // this lane's row in the wave's first stage
+  const int k1 = kb1;
+  MfmaStage<J> sa, sb;
+  int t = 0;
+  if (full > 0) mfma_load<J, false>(sa, xr, w, a.O, k, k1);
+  for (; t + 1 < full; t += 2) {
+    mfma_load<J, false>(sb, xr, w, a.O, k + 64 * (t + 1), k1);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_compute<J>(sa, acc);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_load<J, false>(sa, xr, w, a.O, k + 64 * min(t + 2, full - 1), k1);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_compute<J>(sb, acc);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (t < full) mfma_compute<J>(sa, acc);
+  if (kb0 + 16 * fullTotal < kb1 && fullTotal % 4 == wave) {
+    mfma_load<J, true>(sa, xr, w, a.O, kb0 + 16 * fullTotal + 4 * s, k1);
+    mfma_compute<J>(sa, acc);
+  }
+
+  // Waves 1..3 hand their tiles to wave 0 through LDS; wave 0 adds them in wave order.
+  if (wave > 0) {
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) smem[(((wave - 1) * J + j) * 16 + r) * 64 + lane] = acc[j][r];
+  }
+  __syncthreads();
+  const int rowTiles = (a.B + 31) / 32;
+  float *partial = reinterpret_cast<float *>(a.workspace + counter_bytes(rowTiles * a.tilesN));
+  if (wave == 0) {
+#pragma unroll 1
+    for (int v = 1; v < 4; ++v)
+#pragma unroll
+      for (int j = 0; j < J; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[j][r] += smem[(((v - 1) * J + j) * 16 + r) * 64 + lane];
+    // D[i][c] of MFMA j: i = 8*(r/4) + 4*s + r%4, c = lane%32 -> column n + j.
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int i = rt * 32 + 8 * (r / 4) + 4 * s + (r % 4);
+      if (!colOk) continue;
+      if (a.kSplit > 1) {
+        float *p = partial + long(kg) * rowTiles * 32 * a.O + long(i) * a.O + n;
+#pragma unroll
+        for (int j = 0; j < J; ++j) partial_store(p + j, acc[j][r]);
+      } else if (i < a.B) {
+        float *p = a.dst + long(i) * a.O + n;
+        if constexpr (J == 4) *reinterpret_cast<float4 *>(p) = make_float4(acc[0][r], acc[1][r], acc[2][r], acc[3][r]);
+        else if constexpr (J == 2) *reinterpret_cast<float2 *>(p) = make_float2(acc[0][r], acc[1][r]);
+        else *p = acc[0][r];
+      }
+    }
+  }
+  if (a.kSplit > 1) {
+    unsigned *counters = reinterpret_cast<unsigned *>(a.workspace);
+    if (split_arrive(counters + rt * a.tilesN + tn, a.kSplit, wave))
+      split_finish(a, partial, long(rowTiles) * 32 * a.O, rt * 32, 32, tn * 32 * J, 32 * J);
+  }
+}
+
+// Vector path: lane <-> column; x[B, kChunk slice] staged in LDS; B <= kVectorRows.
+__device__ void linear_vector(const LinearArgs &a, int block, float *smem) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int tn = block % a.tilesN, kg = block / a.tilesN;
+  const int col = tn * 64 + lane;
+  const bool colOk = col < a.O;
+  const int kb0 = kg * a.kChunk, kb1 = min(kb0 + a.kChunk, a.I);
+  float *xs = smem;                                // [B][kChunk]
+  float *red = smem + a.B * a.kChunk;              // [3][B][64]
+  for (int e = threadIdx.x; e < a.B * a.kChunk; e += kBlock) {
+    int r = e / a.kChunk, k = e % a.kChunk;
+    xs[e] = kb0 + k < kb1 ? a.x[long(r) * a.I + kb0 + k] : 0.f;
+  }
+  __syncthreads();
+  const int quarter = a.kChunk / 4;
+  const int k0 = wave * quarter, k1 = min(k0 + quarter, kb1 - kb0);
+  const float *w = a.w + long(a.layer) * a.I * a.O + long(kb0) * a.O + (colOk ? col : 0);
+  float acc[kVectorRows];
+#pragma unroll
+  for (int r = 0; r < kVectorRows; ++r) acc[r] = 0.f;
+  int k = k0;
+  for (; k + 8 <= k1; k += 8) {
+    float wv[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) wv[u] = colOk ? w[long(k + u) * a.O] : 0.f;
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+#pragma unroll
+      for (int r = 0; r < kVectorRows; ++r)
+        if (r < a.B) acc[r] += xs[r * a.kChunk + k + u] * wv[u];
+  }
+  for (; k < k1; ++k) {
+    float wv = colOk ? w[long(k) * a.O] : 0.f;
+#pragma unroll
+    for (int r = 0; r < kVectorRows; ++r)
+      if (r < a.B) acc[r] += xs[r * a.kChunk + k] * wv;
+  }
+  if (wave > 0)
+#pragma unroll
+    for (int r = 0; r < kVectorRows; ++r)
+      if (r < a.B) red[((wave - 1) * a.B + r) * 64 + lane] = acc[r];
+  __syncthreads();
+  float *partial = reinterpret_cast<float *>(a.workspace + counter_bytes(a.tilesN));
+  if (wave == 0 && colOk) {
+#pragma unroll
+    for (int r = 0; r < kVectorRows; ++r) {
+      if (r >= a.B) continue;
+      float v = ((acc[r] + red[r * 64 + lane]) + red[(a.B + r) * 64 + lane]) + red[(2 * a.B + r) * 64 + lane];
+      if (a.kSplit > 1) partial_store(partial + long(kg) * a.B * a.O + long(r) * a.O + col, v);
+      else a.dst[long(r) * a.O + col] = v;
+    }
+  }
+  if (a.kSplit > 1) {
+    unsigned *counters = reinterpret_cast<unsigned *>(a.workspace);
+    if (split_arrive(counters + tn, a.kSplit, wave)) split_finish(a, partial, long(a.B) * a.O, 0, a.B, tn * 64, 64);
+  }
+}
+
+__device__ void linear_body(const LinearArgs &a, int block) {
+  extern __shared__ float smem[];
+  linear_vector(a, block, smem);
+}
+__device__ void linear_mfma1_body(const LinearArgs &a, int block) {
+  extern __shared__ float smem[];
+  linear_mfma<1>(a, block, smem);
+}
+__device__ void linear_mfma4_body(const LinearArgs &a, int block) {
+  extern __shared__ float smem[];
+  linear_mfma<4>(a, block, smem);
+}
 CKL_ENTRY(linear, LinearArgs, linear_body)
+CKL_ENTRY(linear_mfma1, LinearArgs, linear_mfma1_body)
+CKL_ENTRY_ATTR(linear_mfma4, LinearArgs, linear_mfma4_body, CKL_TWO_WAVES)
 
 // ------------------------------------------------------------------ rope
 // Adjacent-pair rotation at position p (workloads.py:72-85):

@@ -1,5 +1,6 @@
 // Host-entry callback ABI (lib/Runtime/NvidiaProgram.cpp:60-108 for the reference's eight
-// callbacks; ckl_module is the HIP addition that selects among several code objects).
+// callbacks; ckl_module is the HIP addition that selects among several code objects, and
+// ckl_workspace gives a library kernel its private zero-initialised device workspace).
 // `frame` is the invocation under construction; errors are recorded in it, never thrown.
 #pragma once
 
@@ -16,4 +17,5 @@ void ckl_argument_resource(void *frame, uint64_t id, uint64_t offset);
 void ckl_argument_value(void *frame, const void *bytes, uint64_t size);
 void ckl_dependency(void *frame, uint64_t id);
 void ckl_commit(void *frame, uint64_t id);
+void ckl_workspace(void *frame, uint64_t bytes);
 }

@@ -557,6 +557,19 @@ extern "C" void ckl_argument_value(void *frame, const void *bytes, uint64_t size
   ckl::rt::callback(frame, [&](Invocation &f) { ckl::rt::appendArgument(f.pending, bytes, size); });
 }
 
+extern "C" void ckl_workspace(void *frame, uint64_t bytes) {
+  ckl::rt::callback(frame, [&](Invocation &f) {
+    if (!bytes) throw std::invalid_argument("library workspace must be non-empty");
+    auto buffer = ckl::rt::allocateBuffer(f.device, bytes);
+    f.device->makeCurrent();
+    ckl::rt::check(hipMemset(reinterpret_cast<void *>(buffer->address()), 0, bytes), "hipMemset(workspace)");
+    ckl::rt::check(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    uint64_t address = buffer->address();
+    ckl::rt::appendArgument(f.pending, &address, sizeof address);
+    f.workspaces.push_back(std::move(buffer));
+  });
+}
+
 extern "C" void ckl_dependency(void *frame, uint64_t id) {
   ckl::rt::callback(frame, [&](Invocation &f) { f.dependencies.push_back(f.nodes.at(id)); });
 }

@@ -92,6 +92,7 @@ struct Invocation {
   hipStream_t stream = nullptr;
   std::vector<std::shared_ptr<Buffer>> heaps;
   std::vector<std::shared_ptr<Buffer>> buffers;     // keeps bound buffers alive
+  std::vector<std::shared_ptr<Buffer>> workspaces;  // private library-kernel workspaces (zeroed at bind)
   std::vector<uint64_t> resources;
   Plan plan;
   hipModule_t module = nullptr;                     // current module during plan construction

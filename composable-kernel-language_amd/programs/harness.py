@@ -148,11 +148,15 @@ class DecoderSession:
         if self.programs[False].prepared_ir != self.programs[True].prepared_ir:
             raise AssertionError("storage ablation changed the prepared device kernels")
 
-    def prefill(self, prompts: np.ndarray, *, mode="graph"):
+    def prefill(self, prompts: np.ndarray, *, mode="graph", progress=None):
         """Teacher-forced device prefill of context-1 steps (reference.py:102-106 semantics):
-        each step runs the decode program, then the next prompt token replaces the argmax."""
+        each step runs the decode program, then the next prompt token replaces the argmax.
+        `progress(done, total)` is called every 128 steps when given."""
         inv = self.invocations[True]
-        for i in range(self.config.context - 1):
+        total = self.config.context - 1
+        for i in range(total):
             inv.run(mode=mode)
             self.state.set_tokens(prompts[i + 1])
+            if progress and (i + 1) % 128 == 0:
+                progress(i + 1, total)
         self.state.snapshot()

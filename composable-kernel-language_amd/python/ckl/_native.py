@@ -88,6 +88,7 @@ _SIGNATURES = {
     "ckl_argument_value": ([ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint64], None),
     "ckl_dependency": ([ctypes.c_void_p, ctypes.c_uint64], None),
     "ckl_commit": ([ctypes.c_void_p, ctypes.c_uint64], None),
+    "ckl_workspace": ([ctypes.c_void_p, ctypes.c_uint64], None),
 }
 EXPORTED = tuple(_SIGNATURES)
 

@@ -227,6 +227,8 @@ class Launch:
     constants: tuple
     block: int = BLOCK
     shared: int = 0
+    entry: str = ""          # entry point when the family has several (default ckl_<name>)
+    workspace: int = 0       # private zero-initialised device workspace bytes (ckl_workspace)
 
 
 def _elementwise(count: int, inner: int) -> int:
@@ -251,12 +253,55 @@ def _rms_apply(shapes, consts, ext):
     return Launch(_elementwise(b * c, c), (b, c, layer))
 
 
+# Tiling of the linear family (csrc/kernels/library.hip, "linear"): output tiles of 64 columns
+# (vector path) or 32*J columns (f32 MFMA path, 32 batch rows per tile), reduction slices of
+# k_chunk rows shared by the 4 waves of a workgroup, and k_split slices combined through the
+# workspace. Measured on MI355X (B = 32): a B = 32 f32 GEMV costs 16 MFMA FLOP per weight byte,
+# so one CU's MFMA rate covers ~38 GB/s of weights and the matrix has to be spread over most of
+# the 256 CUs; but every cross-workgroup split adds a coherent write/read round trip, and one
+# front sweeping the weight rows in address order streams best. Hence: J = 4 (512 B of each
+# weight row per wave) once O alone yields >= 250 tiles, else J = 1, and a split only up to
+# ~256 workgroups with >= 512-row slices.
+LINEAR_TARGET_GROUPS = 256
+LINEAR_VECTOR_ROWS = 16
+
+
+def linear_tiling(b: int, i: int, o: int) -> dict:
+    if b > LINEAR_VECTOR_ROWS and i % 4 == 0 and o % 4 == 0:
+        j = 4 if o >= 16384 else 1
+        tiles = _cdiv(o, 32 * j)
+        split = max(1, min(LINEAR_TARGET_GROUPS // tiles, i // 512))
+        chunk = _cdiv(_cdiv(i, split), 16) * 16
+        split = _cdiv(i, chunk)
+        rows, row_tiles = _cdiv(b, 32) * 32, _cdiv(b, 32)
+        shared = 3 * j * 16 * 64 * 4
+        entry = f"ckl_linear_mfma{j}"
+    elif b <= LINEAR_VECTOR_ROWS:
+        tiles = _cdiv(o, 64)
+        chunk = min(_cdiv(i, 4) * 4, 128)
+        split = _cdiv(i, chunk)
+        rows, row_tiles = b, 1
+        shared = (b * chunk + 3 * b * 64) * 4
+        entry = "ckl_linear"
+    else:
+        return None
+    workspace = 256
+    if split > 1:
+        workspace = _cdiv(4 * row_tiles * tiles, 256) * 256 + 4 * split * rows * o
+    return dict(grid=row_tiles * split * tiles, tiles=tiles, split=split, chunk=chunk, shared=shared, entry=entry,
+                workspace=workspace)
+
+
 def _linear(shapes, consts, ext):
     (b, i), (w, _i, o) = shapes[0], shapes[1]
     layer = consts[3]
     if not (0 <= layer < w) or not (ext[0] >= o and ext[1:] == (b, 1)):
         return None
-    return Launch(_cdiv(o, 64), (b, i, o, layer))
+    t = linear_tiling(b, i, o)
+    if t is None:
+        return None
+    return Launch(t["grid"], (b, i, o, layer, t["tiles"], t["split"], t["chunk"], 0), shared=t["shared"],
+                  entry=t["entry"], workspace=t["workspace"])
 
 
 def _rope(shapes, consts, ext):
@@ -397,8 +442,10 @@ def selection_attribute(selections: dict, artifact: str) -> str:
     for symbol, s in sorted(selections.items()):
         fields = [f'artifact = "{artifact}"', f"block = array<i64: {s.launch.block}, 1, 1>",
                   "constants = [" + ", ".join(f"{int(c)} : i32" for c in s.launch.constants) + "]",
-                  f'entry_point = "{s.kernel.entry_point}"', f"grid = array<i64: {s.launch.grid}, 1, 1>",
+                  f'entry_point = "{s.launch.entry or s.kernel.entry_point}"', f"grid = array<i64: {s.launch.grid}, 1, 1>",
                   f'implementation = "ckl.hip.library.{s.kernel.name}"', f"shared_memory = {s.launch.shared} : i64"]
+        if s.launch.workspace:
+            fields.append(f"workspace = {s.launch.workspace} : i64")
         if s.kernel.groupable:
             fields.append(f'group = "{s.kernel.name}"')
         entries.append(f"{symbol} = {{{', '.join(sorted(fields))}}}")

@@ -149,7 +149,7 @@ void ckl_invocation_release(ckl_invocation *invocation);
 /* ---------------------------------------------------------------- host-entry callbacks
  * The reference's eight callbacks with identical signatures (NvidiaProgram.cpp:60-108) plus
  * ckl_module, which loads (once per device) and selects a named code object so one plan can
- * mix library kernels and JIT-compiled kernels. Errors are recorded in `frame`; later
+ * mix library kernels and JIT-compiled kernels, and ckl_workspace (below). Errors are recorded in `frame`; later
  * callbacks become no-ops and ckl_bind reports the first error. */
 void ckl_begin(void *frame, const void *binary, uint64_t bytes);
 void ckl_module(void *frame, const char *identity, const void *binary, uint64_t bytes);
@@ -161,6 +161,12 @@ void ckl_argument_resource(void *frame, uint64_t id, uint64_t offset);
 void ckl_argument_value(void *frame, const void *bytes, uint64_t size);
 void ckl_dependency(void *frame, uint64_t id);
 void ckl_commit(void *frame, uint64_t id);
+/* HIP addition (no reference counterpart): gives the pending kernel a private device workspace of
+ * `bytes` bytes, zero-filled once at bind and owned by the invocation, and appends its address
+ * as the next kernel argument. Library kernels that combine partial results across workgroups
+ * (split reductions with self-resetting completion counters) use it; the reference's kernels
+ * never need one. */
+void ckl_workspace(void *frame, uint64_t bytes);
 
 #ifdef __cplusplus
 }
