@@ -159,6 +159,11 @@ def run_config(name, c, args, device):
     return session, result, final
 
 
+def c_name(c):
+    from programs.decoder_config import CONFIGS
+    return next((k for k, v in CONFIGS.items() if (v.batch, v.hidden, v.layers, v.vocab) == (c.batch, c.hidden, c.layers, c.vocab)), None)
+
+
 def kernel_roofline(session, c, iterations=10):
     """Time every plan node of one step with HIP events (back-to-back launches of the node on the
     invocation stream) and return per-family totals and the roofline entry of the dominant family
@@ -195,7 +200,7 @@ def kernel_roofline(session, c, iterations=10):
     roofline = {"bound": "hbm", "kernel": f"ckl_{dominant}", "achieved": achieved / 1e9, "peak": HBM_PEAK / 1e9,
                 "unit": "GB/s", "frac": achieved / HBM_PEAK, "traffic": None,
                 "algorithmic_bytes_per_launch": per_launch, "avg_launch_us": avg,
-                "config": "large", "position": position}
+                "config": c_name(c), "position": position}
     return summary, dominant, roofline
 
 
@@ -271,13 +276,13 @@ def main():
     for name in args.configs:
         c = dataclasses.replace(CONFIGS[name], steps=args.steps)
         session, result, final = run_config(name, c, args, device)
+        summary, dominant, roofline = kernel_roofline(session, c)
+        result["kernels"] = summary
+        for family, row in summary.items():
+            log(f"[{name}] {family:18s} launches={row['launches']:3d} avg={row['avg_us']:9.2f} us "
+                f"total={row['total_us']:9.2f} us  {row['achieved_GBps']:8.1f} GB/s")
         if name == "large":
-            summary, dominant, roofline = kernel_roofline(session, c)
-            result["kernels"] = summary
             result["roofline"] = roofline
-            for family, row in summary.items():
-                log(f"[large] {family:18s} launches={row['launches']:3d} avg={row['avg_us']:9.2f} us "
-                    f"total={row['total_us']:9.2f} us  {row['achieved_GBps']:8.1f} GB/s")
             log(f"[large] dominant kernel {dominant}: {roofline}")
         if not args.no_cpu_baseline and name in ("small",):
             result["cpu_baseline"] = cpu_baseline(session, c, final)

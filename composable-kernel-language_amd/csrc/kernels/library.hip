@@ -26,14 +26,14 @@ template <typename Args> struct CKL_ALIGN Group {
   int count;
 };
 
-#define CKL_ENTRY_ATTR(name, Args, body, attributes)                                                 \
-  extern "C" __global__ __launch_bounds__(kBlock) attributes void ckl_##name(const Args a) { body(a, blockIdx.x); } \
-  extern "C" __global__ __launch_bounds__(kBlock) attributes void ckl_##name##_group(const Group<Args> g) { \
+#define CKL_ENTRY_ATTR(name, Args, body, threads, attributes)                                        \
+  extern "C" __global__ __launch_bounds__(threads) attributes void ckl_##name(const Args a) { body(a, blockIdx.x); } \
+  extern "C" __global__ __launch_bounds__(threads) attributes void ckl_##name##_group(const Group<Args> g) { \
     int b = blockIdx.x, m = 0;                                                                        \
     while (m + 1 < g.count && b >= g.start[m + 1]) ++m;                                               \
     body(g.m[m], b - g.start[m]);                                                                     \
   }
-#define CKL_ENTRY(name, Args, body) CKL_ENTRY_ATTR(name, Args, body, )
+#define CKL_ENTRY(name, Args, body) CKL_ENTRY_ATTR(name, Args, body, kBlock, )
 // Streaming kernels that keep several loads in flight per lane trade occupancy for registers.
 #define CKL_TWO_WAVES __attribute__((amdgpu_waves_per_eu(1, 2)))
 
@@ -172,8 +172,8 @@ CKL_ENTRY(rms_apply, RmsApplyArgs, rms_apply_body)
 // rowTiles x kSplit x tilesN workgroups of 256 threads (4 waves): workgroup (rt, kg, tn) owns
 // output tile tn (a column range) for batch-row tile rt over the reduction slice
 // [kg*kChunk, (kg+1)*kChunk), which its 4 waves share.
-//   ckl_linear (vector, B <= 16): lane <-> output column (64 per tile), rows accumulated in
-//           VGPRs, x staged through LDS;
+//   ckl_linear_rowvec (vector, B <= 16): one batch row and 64 output columns (lane <-> column)
+//           per workgroup, the reduction split over its waves;
 //   ckl_linear_mfma1/4 (f32 MFMA, B > 16): v_mfma_f32_32x32x2f32 over 32 batch rows; each lane loads
 //           J = 1 / 4 consecutive weight columns with one vector load, and MFMA j accumulates
 //           columns {J*c + j}, so one wave owns a 32 x 32J tile. The K index is permuted so the
@@ -190,14 +190,23 @@ struct CKL_ALIGN LinearArgs {
   int tilesN, kSplit, kChunk, pad;
   unsigned char *workspace;
 };
-constexpr int kVectorRows = 16;
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 // s_waitcnt immediate (gfx9 encoding) that waits for vmcnt == 0 only: outstanding vector memory
 // operations of the wave, stores included, have completed.
 constexpr int kWaitStores = 0x0F70;
 
+// Workspace layout of the linear family: kZeroPage bytes that stay zero (loads of padding read
+// here, so they need neither a predicate nor a select on the loaded value), then the split
+// completion counters (padded to 256 B), then the partial tiles.
+constexpr int kZeroPage = 256;
 __device__ __forceinline__ int counter_bytes(int count) { return (count * 4 + 255) & ~255; }
+__device__ __forceinline__ unsigned *split_counters(const LinearArgs &a) {
+  return reinterpret_cast<unsigned *>(a.workspace + kZeroPage);
+}
+__device__ __forceinline__ float *split_partials(const LinearArgs &a, int counters) {
+  return reinterpret_cast<float *>(a.workspace + kZeroPage + counter_bytes(counters));
+}
 
 // Cross-workgroup partial tiles live in the workspace and are written and read only with
 // agent-scope atomic stores/loads (sc1: coherent across the MI355X's per-XCD L2 caches without
@@ -229,14 +238,24 @@ __device__ __forceinline__ bool split_arrive(unsigned *counter, int parts, int w
 }
 
 // Adds the kSplit partial tiles (rows [r0, r0+rows), columns [c0, c0+cols)) in split order
-// and writes dst.
+// and writes dst. The partials of kFinishBatch splits are loaded together, then added in order
+// (the batch condition is uniform; agent-coherent loads of one address serialize, so indices past
+// the end are skipped rather than clamped).
+constexpr int kFinishBatch = 8;
 __device__ void split_finish(const LinearArgs &a, const float *partial, long planeStride, int r0, int rows, int c0,
                              int cols) {
-  for (int e = threadIdx.x; e < rows * cols; e += kBlock) {
+  for (int e = threadIdx.x; e < rows * cols; e += blockDim.x) {
     int r = r0 + e / cols, c = c0 + e % cols;
     if (r >= a.B || c >= a.O) continue;
+    const float *p = partial + long(r) * a.O + c;
     float total = 0.f;
-    for (int g = 0; g < a.kSplit; ++g) total += partial_load(partial + g * planeStride + long(r) * a.O + c);
+    for (int g0 = 0; g0 < a.kSplit; g0 += kFinishBatch) {
+      float v[kFinishBatch];
+#pragma unroll
+      for (int j = 0; j < kFinishBatch; ++j) v[j] = g0 + j < a.kSplit ? partial_load(p + (g0 + j) * planeStride) : 0.f;
+#pragma unroll
+      for (int j = 0; j < kFinishBatch; ++j) total += v[j];
+    }
     a.dst[long(r) * a.O + c] = total;
   }
 }
@@ -358,7 +377,7 @@ template <int J> __device__ void linear_mfma(const LinearArgs &a, int block, flo
   }
   __syncthreads();
   const int rowTiles = (a.B + 31) / 32;
-  float *partial = reinterpret_cast<float *>(a.workspace + counter_bytes(rowTiles * a.tilesN));
+  float *partial = split_partials(a, rowTiles * a.tilesN);
   if (wave == 0) {
 #pragma unroll 1
     for (int v = 1; v < 4; ++v)
@@ -384,74 +403,66 @@ template <int J> __device__ void linear_mfma(const LinearArgs &a, int block, flo
     }
   }
   if (a.kSplit > 1) {
-    unsigned *counters = reinterpret_cast<unsigned *>(a.workspace);
+    unsigned *counters = split_counters(a);
     if (split_arrive(counters + rt * a.tilesN + tn, a.kSplit, wave))
       split_finish(a, partial, long(rowTiles) * 32 * a.O, rt * 32, 32, tn * 32 * J, 32 * J);
   }
 }
 
-// Vector path: lane <-> column; x[B, kChunk slice] staged in LDS; B <= kVectorRows.
-__device__ void linear_vector(const LinearArgs &a, int block, float *smem) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int tn = block % a.tilesN, kg = block / a.tilesN;
+// Row-parallel vector path (B <= 16, latency-bound): workgroup (tn, b, kg) computes the 64
+// outputs dst[b, 64*tn .. 64*tn+63] (lane <-> column) over the reduction slice kg of waves*64 rows;
+// wave w owns 64 consecutive rows of it. Measured on MI355X, these few-microsecond kernels are
+// bound by memory round trips and by the instruction count of the busiest wave, so each wave
+// issues all 64 of its weight loads at once (unpredicated: a predicated load becomes its own
+// round trip because the compiler drains the load queue where branches join; padding rows read
+// the workspace's zero page), takes x[b, k] as wave-uniform scalar loads, and does 64 FMAs.
+// Waves are combined through LDS in wave order; only reductions longer than 16*64 rows split
+// across workgroups.
+constexpr int kVectorRows = 64;
+constexpr int kVectorWaves = 16;
+__device__ void linear_rowvec_body(const LinearArgs &a, int block) {
+  __shared__ float red[kVectorWaves][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int waves = blockDim.x >> 6;
+  const int tn = block % a.tilesN, rest = block / a.tilesN;
+  const int b = rest % a.B, kg = rest / a.B;
   const int col = tn * 64 + lane;
   const bool colOk = col < a.O;
-  const int kb0 = kg * a.kChunk, kb1 = min(kb0 + a.kChunk, a.I);
-  float *xs = smem;                                // [B][kChunk]
-  float *red = smem + a.B * a.kChunk;              // [3][B][64]
-  for (int e = threadIdx.x; e < a.B * a.kChunk; e += kBlock) {
-    int r = e / a.kChunk, k = e % a.kChunk;
-    xs[e] = kb0 + k < kb1 ? a.x[long(r) * a.I + kb0 + k] : 0.f;
+  const int span = waves * kVectorRows;
+  const int kb0 = kg * span, kb1 = min(kb0 + span, a.I);
+  const int k0 = kb0 + wave * kVectorRows, k1 = min(k0 + kVectorRows, kb1);
+  const float *zero = reinterpret_cast<const float *>(a.workspace);   // kZeroPage: 64 zero floats
+  const float *__restrict__ xr = a.x + long(b) * a.I;
+  const float *w = a.w + long(a.layer) * a.I * a.O + long(k0) * a.O + (colOk ? col : 0);
+  float acc = 0.f;
+  if (k1 - k0 == kVectorRows) {
+    float wv[kVectorRows];
+#pragma unroll
+    for (int u = 0; u < kVectorRows; ++u) wv[u] = w[long(u) * a.O];
+#pragma unroll
+    for (int u = 0; u < kVectorRows; ++u) acc += xr[k0 + u] * wv[u];
+  } else if (k0 < k1) {
+    float wv[kVectorRows];
+#pragma unroll
+    for (int u = 0; u < kVectorRows; ++u) wv[u] = *(k0 + u < k1 ? w + long(u) * a.O : zero + lane);
+#pragma unroll
+    for (int u = 0; u < kVectorRows; ++u) acc += (k0 + u < k1 ? xr[min(k0 + u, k1 - 1)] : 0.f) * wv[u];
   }
+  red[wave][lane] = acc;
   __syncthreads();
-  const int quarter = a.kChunk / 4;
-  const int k0 = wave * quarter, k1 = min(k0 + quarter, kb1 - kb0);
-  const float *w = a.w + long(a.layer) * a.I * a.O + long(kb0) * a.O + (colOk ? col : 0);
-  float acc[kVectorRows];
-#pragma unroll
-  for (int r = 0; r < kVectorRows; ++r) acc[r] = 0.f;
-  int k = k0;
-  for (; k + 8 <= k1; k += 8) {
-    float wv[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) wv[u] = colOk ? w[long(k + u) * a.O] : 0.f;
-#pragma unroll
-    for (int u = 0; u < 8; ++u)
-#pragma unroll
-      for (int r = 0; r < kVectorRows; ++r)
-        if (r < a.B) acc[r] += xs[r * a.kChunk + k + u] * wv[u];
+  if (wave != 0 || !colOk) {
+    if (a.kSplit == 1) return;
+  } else {
+    float v = red[0][lane];
+    for (int v2 = 1; v2 < waves; ++v2) v += red[v2][lane];
+    if (a.kSplit > 1) partial_store(split_partials(a, a.B * a.tilesN) + (long(kg) * a.B + b) * a.O + col, v);
+    else a.dst[long(b) * a.O + col] = v;
   }
-  for (; k < k1; ++k) {
-    float wv = colOk ? w[long(k) * a.O] : 0.f;
-#pragma unroll
-    for (int r = 0; r < kVectorRows; ++r)
-      if (r < a.B) acc[r] += xs[r * a.kChunk + k] * wv;
-  }
-  if (wave > 0)
-#pragma unroll
-    for (int r = 0; r < kVectorRows; ++r)
-      if (r < a.B) red[((wave - 1) * a.B + r) * 64 + lane] = acc[r];
-  __syncthreads();
-  float *partial = reinterpret_cast<float *>(a.workspace + counter_bytes(a.tilesN));
-  if (wave == 0 && colOk) {
-#pragma unroll
-    for (int r = 0; r < kVectorRows; ++r) {
-      if (r >= a.B) continue;
-      float v = ((acc[r] + red[r * 64 + lane]) + red[(a.B + r) * 64 + lane]) + red[(2 * a.B + r) * 64 + lane];
-      if (a.kSplit > 1) partial_store(partial + long(kg) * a.B * a.O + long(r) * a.O + col, v);
-      else a.dst[long(r) * a.O + col] = v;
-    }
-  }
-  if (a.kSplit > 1) {
-    unsigned *counters = reinterpret_cast<unsigned *>(a.workspace);
-    if (split_arrive(counters + tn, a.kSplit, wave)) split_finish(a, partial, long(a.B) * a.O, 0, a.B, tn * 64, 64);
-  }
+  if (a.kSplit > 1 && split_arrive(split_counters(a) + b * a.tilesN + tn, a.kSplit, wave))
+    split_finish(a, split_partials(a, a.B * a.tilesN), long(a.B) * a.O, b, 1, tn * 64, 64);
 }
 
-__device__ void linear_body(const LinearArgs &a, int block) {
-  extern __shared__ float smem[];
-  linear_vector(a, block, smem);
-}
 __device__ void linear_mfma1_body(const LinearArgs &a, int block) {
   extern __shared__ float smem[];
   linear_mfma<1>(a, block, smem);
@@ -460,9 +471,9 @@ __device__ void linear_mfma4_body(const LinearArgs &a, int block) {
   extern __shared__ float smem[];
   linear_mfma<4>(a, block, smem);
 }
-CKL_ENTRY(linear, LinearArgs, linear_body)
+CKL_ENTRY_ATTR(linear_rowvec, LinearArgs, linear_rowvec_body, 1024, )
 CKL_ENTRY(linear_mfma1, LinearArgs, linear_mfma1_body)
-CKL_ENTRY_ATTR(linear_mfma4, LinearArgs, linear_mfma4_body, CKL_TWO_WAVES)
+CKL_ENTRY_ATTR(linear_mfma4, LinearArgs, linear_mfma4_body, kBlock, CKL_TWO_WAVES)
 
 // ------------------------------------------------------------------ rope
 // Adjacent-pair rotation at position p (workloads.py:72-85):
@@ -513,8 +524,12 @@ CKL_ENTRY(append_kv, AppendArgs, append_kv_body)
 
 // ------------------------------------------------------------------ attention_scores
 // scores[b,h,t] = (sum_d q[b,h*D+d] * kc[layer,b,h,t,d]) * scale for t <= p (workloads.py:100-111).
-// One block per (b, h, 256-row chunk); lane groups of D/4 lanes reduce one cache row each.
+// One 256-thread workgroup per (b, h, 256-row chunk); each wave owns 64 consecutive cache rows.
+// Groups of D/4 lanes hold one row as float4s; a wave issues kScoreBatch row loads per lane before
+// reducing any of them, so ~kScoreBatch KB per wave are in flight. Row addresses past the end
+// re-read an early row of the wave and their results are dropped (the loads stay unpredicated).
 struct CKL_ALIGN ScoresArgs { const float *q; const float *kc; const int *position; float *scores; float scale; int L, B, A, T, D, layer; };
+constexpr int kScoreBatch = 8;
 __device__ void attention_scores_body(const ScoresArgs &a, int block) {
   int chunks = (a.T + kBlock - 1) / kBlock;
   int chunk = block % chunks;
@@ -529,25 +544,33 @@ __device__ void attention_scores_body(const ScoresArgs &a, int block) {
   float *scores = a.scores + bh * a.T;
   int tEnd = min(t0 + kBlock, end);
   if ((a.D & 3) == 0 && a.D <= 256 && (64 % (a.D / 4)) == 0) {
-    int width = a.D / 4;                         // lanes per row
-    int rowsPerWave = 64 / width;
-    int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    int sub = lane / width, part = lane % width;
-    float4 qv = reinterpret_cast<const float4 *>(q)[part];
-    for (int t = t0 + wave * rowsPerWave + sub; t - sub < tEnd; t += 4 * rowsPerWave) {
-      float s = 0.f;
-      if (t < tEnd) {
-        float4 kv = reinterpret_cast<const float4 *>(keys + long(t) * a.D)[part];
-        s = qv.x * kv.x + qv.y * kv.y + qv.z * kv.z + qv.w * kv.w;
+    const int width = a.D / 4;                   // lanes per row
+    const int rowsPerLoad = 64 / width;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int sub = lane / width, part = lane % width;
+    const float4 qv = reinterpret_cast<const float4 *>(q)[part];
+    const int w0 = t0 + wave * 64, w1 = min(w0 + 64, tEnd);
+    for (int base = w0; base < w1; base += kScoreBatch * rowsPerLoad) {
+      float4 kv[kScoreBatch];
+#pragma unroll
+      for (int u = 0; u < kScoreBatch; ++u) {
+        int t = base + u * rowsPerLoad + sub;
+        t = t < w1 ? t : min(w0 + sub, w1 - 1);    // past the end: re-read an early row, dropped
+        kv[u] = reinterpret_cast<const float4 *>(keys + long(t) * a.D)[part];
       }
-      s = group_sum(s, width);
-      if (part == 0 && t < tEnd) scores[t] = s * a.scale;
+#pragma unroll
+      for (int u = 0; u < kScoreBatch; ++u) {
+        float v = qv.x * kv[u].x + qv.y * kv[u].y + qv.z * kv[u].z + qv.w * kv[u].w;
+        v = group_sum(v, width);
+        int t = base + u * rowsPerLoad + sub;
+        if (part == 0 && t < w1) scores[t] = v * a.scale;
+      }
     }
   } else {
     for (int t = t0 + threadIdx.x; t < tEnd; t += kBlock) {
-      float s = 0.f;
-      for (int d = 0; d < a.D; ++d) s += q[d] * keys[long(t) * a.D + d];
-      scores[t] = s * a.scale;
+      float v = 0.f;
+      for (int d = 0; d < a.D; ++d) v += q[d] * keys[long(t) * a.D + d];
+      scores[t] = v * a.scale;
     }
   }
 }
@@ -555,49 +578,108 @@ CKL_ENTRY(attention_scores, ScoresArgs, attention_scores_body)
 
 // ------------------------------------------------------------------ softmax
 // probs[b,h,t] = exp(s[t] - max) / sum_t' exp(s[t'] - max) over t <= p (workloads.py:114-128).
-// One wave per (b, h) row.
-struct CKL_ALIGN SoftmaxArgs { const float *scores; const int *position; float *probs; int B, A, T; };
+// `rowThreads` (64 or 256) lanes per (b, h) row; each lane keeps up to kSoftmaxPerLane scores in
+// registers (one read of the row, one write), longer rows stream three passes.
+struct CKL_ALIGN SoftmaxArgs { const float *scores; const int *position; float *probs; int B, A, T, rowThreads; };
+constexpr int kSoftmaxPerLane = 8;
+
+// Reduction over the `rowThreads` lanes of one row (a wave, or the whole 4-wave workgroup).
+template <bool IsMax> __device__ __forceinline__ float row_reduce(float v, int rowThreads) {
+  __shared__ float across[kBlock / 64];
+  v = IsMax ? wave_max(v) : wave_sum(v);
+  if (rowThreads <= 64) return v;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) across[wave] = v;
+  __syncthreads();
+  float r = across[0];
+  for (int w = 1; w < kBlock / 64; ++w) r = IsMax ? fmaxf(r, across[w]) : r + across[w];
+  return r;
+}
+
 __device__ void softmax_body(const SoftmaxArgs &a, int block) {
-  int lane = threadIdx.x & 63;
-  long row = long(block) * (kBlock / 64) + (threadIdx.x >> 6);
-  if (row >= long(a.B) * a.A) return;
+  const int rowsPerBlock = kBlock / a.rowThreads;
+  const int local = threadIdx.x % a.rowThreads;
+  long row = long(block) * rowsPerBlock + threadIdx.x / a.rowThreads;
+  const bool active = row < long(a.B) * a.A;       // uniform per row group (rowThreads divides kBlock)
   int p = load_position(a.position);
   int end = min(p + 1, a.T);
-  if (p < 0) return;
-  const float *s = a.scores + row * a.T;
-  float *out = a.probs + row * a.T;
-  float m = -__builtin_inff();
-  for (int t = lane; t < end; t += 64) m = fmaxf(m, s[t]);
-  m = wave_max(m);
-  float total = 0.f;
-  for (int t = lane; t < end; t += 64) total += expf(s[t] - m);
-  total = wave_sum(total);
-  for (int t = lane; t < end; t += 64) out[t] = expf(s[t] - m) / total;
+  if (p < 0) end = 0;
+  const float *s = a.scores + (active ? row : 0) * a.T;
+  float *out = a.probs + (active ? row : 0) * a.T;
+  if (end <= a.rowThreads * kSoftmaxPerLane) {
+    float v[kSoftmaxPerLane];
+    float m = -__builtin_inff();
+#pragma unroll
+    for (int u = 0; u < kSoftmaxPerLane; ++u) {
+      int t = local + u * a.rowThreads;
+      v[u] = active && t < end ? s[t] : -__builtin_inff();
+      m = fmaxf(m, v[u]);
+    }
+    m = row_reduce<true>(m, a.rowThreads);
+    float total = 0.f;
+#pragma unroll
+    for (int u = 0; u < kSoftmaxPerLane; ++u) {
+      int t = local + u * a.rowThreads;
+      v[u] = t < end ? expf(v[u] - m) : 0.f;
+      total += v[u];
+    }
+    total = row_reduce<false>(total, a.rowThreads);
+#pragma unroll
+    for (int u = 0; u < kSoftmaxPerLane; ++u) {
+      int t = local + u * a.rowThreads;
+      if (active && t < end) out[t] = v[u] / total;
+    }
+  } else {
+    float m = -__builtin_inff();
+    for (int t = local; t < end; t += a.rowThreads) m = fmaxf(m, active ? s[t] : -__builtin_inff());
+    m = row_reduce<true>(m, a.rowThreads);
+    float total = 0.f;
+    for (int t = local; t < end; t += a.rowThreads) total += active ? expf(s[t] - m) : 0.f;
+    total = row_reduce<false>(total, a.rowThreads);
+    for (int t = local; t < end; t += a.rowThreads)
+      if (active) out[t] = expf(s[t] - m) / total;
+  }
 }
 CKL_ENTRY(softmax, SoftmaxArgs, softmax_body)
 
 // ------------------------------------------------------------------ attention_values
 // dst[b, h*D+d] = sum_{t<=p} probs[b,h,t] * vc[layer,b,h,t,d]   (workloads.py:131-142).
-// One block per (b, h): lane groups of D/4 lanes own a float4 column slice; 256/(D/4) row
-// groups stride over t; partial float4 sums are combined through LDS in a fixed order.
+// One workgroup per (b, h) of blockDim.x <= kValuesBlock threads (a power of two, chosen from the
+// cache capacity): groups of D/4 lanes own the float4 column slices of one row, blockDim/(D/4)
+// row groups stride over t with kValuesBatch row loads per lane in flight; the partial float4
+// sums are combined by a fixed-order tree in LDS.
 struct CKL_ALIGN ValuesArgs { const float *probs; const float *vc; const int *position; float *dst; int L, B, A, T, D, layer; };
+constexpr int kValuesBlock = 512;
+constexpr int kValuesBatch = 8;
 __device__ void attention_values_body(const ValuesArgs &a, int block) {
-  __shared__ float4 partial[kBlock];
+  __shared__ float4 partial[kValuesBlock];
   long bh = block;
   if (bh >= long(a.B) * a.A) return;
   int p = load_position(a.position);
   int end = min(p + 1, a.T);
+  if (p < 0) end = 0;
   const float *probs = a.probs + bh * a.T;
   const float *values = a.vc + (long(a.layer) * a.B * a.A + bh) * long(a.T) * a.D;
   float *dst = a.dst + bh * a.D;
-  if ((a.D & 3) == 0 && a.D <= 4 * kBlock && (kBlock % (a.D / 4)) == 0) {
-    int width = a.D / 4, groups = kBlock / width;
-    int g = threadIdx.x / width, part = threadIdx.x % width;
+  if ((a.D & 3) == 0 && a.D <= 4 * 64 && (64 % (a.D / 4)) == 0) {
+    const int width = a.D / 4, groups = int(blockDim.x) / width;
+    const int g = threadIdx.x / width, part = threadIdx.x % width;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int t = g; t < end && p >= 0; t += groups) {
-      float pr = probs[t];
-      float4 v = reinterpret_cast<const float4 *>(values + long(t) * a.D)[part];
-      acc.x += pr * v.x; acc.y += pr * v.y; acc.z += pr * v.z; acc.w += pr * v.w;
+    for (int base = 0; base < end; base += kValuesBatch * groups) {
+      float4 v[kValuesBatch];
+      float pr[kValuesBatch];
+#pragma unroll
+      for (int u = 0; u < kValuesBatch; ++u) {
+        int t = base + u * groups + g;
+        int tc = t < end ? t : min(g, end - 1);    // past the end: re-read an early row, weight 0
+        v[u] = reinterpret_cast<const float4 *>(values + long(tc) * a.D)[part];
+        pr[u] = t < end ? probs[tc] : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < kValuesBatch; ++u) {
+        acc.x += pr[u] * v[u].x; acc.y += pr[u] * v[u].y; acc.z += pr[u] * v[u].z; acc.w += pr[u] * v[u].w;
+      }
     }
     partial[threadIdx.x] = acc;
     __syncthreads();
@@ -611,14 +693,14 @@ __device__ void attention_values_body(const ValuesArgs &a, int block) {
     }
     if (g == 0) reinterpret_cast<float4 *>(dst)[part] = partial[part];
   } else {
-    for (int d = threadIdx.x; d < a.D; d += kBlock) {
+    for (int d = threadIdx.x; d < a.D; d += blockDim.x) {
       float acc = 0.f;
-      for (int t = 0; t < end && p >= 0; ++t) acc += probs[t] * values[long(t) * a.D + d];
+      for (int t = 0; t < end; ++t) acc += probs[t] * values[long(t) * a.D + d];
       dst[d] = acc;
     }
   }
 }
-CKL_ENTRY(attention_values, ValuesArgs, attention_values_body)
+CKL_ENTRY_ATTR(attention_values, ValuesArgs, attention_values_body, kValuesBlock, )
 
 // ------------------------------------------------------------------ pointwise
 // add: dst = x + y; multiply: dst = x * y; silu: dst = v / (1 + exp(-v)) (workloads.py:145-167).
@@ -657,33 +739,71 @@ __device__ void silu_body(const UnaryArgs &a, int block) {
 CKL_ENTRY(silu, UnaryArgs, silu_body)
 
 // ------------------------------------------------------------------ greedy
-// tokens[b] = history[p, b] = first index of the maximum logit (strict '>' scan,
-// workloads.py:170-183). One block per row; NaN logits never win unless at index 0.
-struct CKL_ALIGN GreedyArgs { const float *logits; int *tokens; int *history; const int *position; int B, V, T; };
+// tokens[b] = history[p, b] = first index of the maximum logit (strict '>' scan from index 0,
+// workloads.py:170-183): NaN logits never win, a NaN logit 0 is never displaced, +0 and -0 tie.
+// Each row is cut into `chunks` slices of kGreedyChunk logits, one 256-thread workgroup each.
+// A workgroup reduces its slice to a (value, index) pair; with one slice it writes the token,
+// otherwise it folds the pair into the row's 64-bit key (ordered value bits << 32 | ~index, so
+// the maximum key is the largest value at the smallest index) with an agent-scope atomic max
+// and bumps the row's counter; the last workgroup writes the token and resets key and counter.
+// workspace: uint64 key[B], then uint32 counter[B].
+struct CKL_ALIGN GreedyArgs {
+  const float *logits; int *tokens; int *history; const int *position; int B, V, T, chunks;
+  unsigned char *workspace;
+};
+constexpr int kGreedyChunk = 4096;
+
+__device__ __forceinline__ unsigned long long greedy_key(float v, int index) {
+  unsigned bits = __float_as_uint(v == 0.f ? 0.f : v);     // -0 ties with +0
+  unsigned ordered = (bits & 0x80000000u) ? ~bits : (bits | 0x80000000u);
+  return (static_cast<unsigned long long>(ordered) << 32) | (0xFFFFFFFFu - unsigned(index));
+}
+
 __device__ void greedy_body(const GreedyArgs &a, int block) {
-  __shared__ float bestValue[kBlock / 64];
-  __shared__ int bestIndex[kBlock / 64];
-  int b = block;
+  __shared__ unsigned long long bestKey[kBlock / 64];
+  const int b = block / a.chunks, chunk = block % a.chunks;
   if (b >= a.B) return;
   const float *logits = a.logits + long(b) * a.V;
-  float v = -__builtin_inff();
-  int idx = 0x7fffffff;
-  for (int k = threadIdx.x; k < a.V; k += kBlock) {
-    float x = logits[k];
-    if (x > v || (x == v && k < idx)) { v = x; idx = k; }
+  const int v0 = chunk * kGreedyChunk, v1 = min(v0 + kGreedyChunk, a.V);
+  unsigned long long key = 0;                               // below every real key
+  float x[kGreedyChunk / kBlock];
+#pragma unroll
+  for (int u = 0; u < kGreedyChunk / kBlock; ++u) x[u] = logits[min(v0 + u * kBlock + int(threadIdx.x), v1 - 1)];
+#pragma unroll
+  for (int u = 0; u < kGreedyChunk / kBlock; ++u) {
+    int k = v0 + u * kBlock + threadIdx.x;
+    if (k < v1 && x[u] == x[u]) key = max(key, greedy_key(x[u], k));
   }
-  wave_argmax(v, idx);
-  int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  if (lane == 0) { bestValue[wave] = v; bestIndex[wave] = idx; }
+#pragma unroll
+  for (int offset = 32; offset > 0; offset /= 2) {
+    unsigned long long other = __shfl_xor(key, offset);
+    key = max(key, other);
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) bestKey[wave] = key;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    for (int w = 1; w < kBlock / 64; ++w) argmax_combine(v, idx, bestValue[w], bestIndex[w]);
-    float first = logits[0];
-    int winner = first != first ? 0 : idx;   // a NaN first logit is never displaced
-    int p = load_position(a.position);
-    a.tokens[b] = winner;
-    if (p >= 0 && p < a.T) a.history[long(p) * a.B + b] = winner;
+  if (threadIdx.x != 0) return;
+  for (int w = 1; w < kBlock / 64; ++w) key = max(key, bestKey[w]);
+  bool finish = a.chunks == 1;
+  if (!finish) {
+    unsigned long long *keys = reinterpret_cast<unsigned long long *>(a.workspace);
+    unsigned *counters = reinterpret_cast<unsigned *>(a.workspace + 8 * a.B);
+    __hip_atomic_fetch_max(keys + b, key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(kWaitStores);
+    unsigned previous = __hip_atomic_fetch_add(counters + b, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    finish = previous == unsigned(a.chunks - 1);
+    if (finish) {
+      key = __hip_atomic_load(keys + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(keys + b, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(counters + b, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
+  if (!finish) return;
+  float first = logits[0];
+  int winner = (first != first || key == 0) ? 0 : int(0xFFFFFFFFu - unsigned(key & 0xFFFFFFFFu));
+  int p = load_position(a.position);
+  a.tokens[b] = winner;
+  if (p >= 0 && p < a.T) a.history[long(p) * a.B + b] = winner;
 }
 CKL_ENTRY(greedy, GreedyArgs, greedy_body)
 

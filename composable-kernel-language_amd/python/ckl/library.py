@@ -215,6 +215,8 @@ def update(src: _Vector, dst: _Vector, bias: ckl.f32) -> None:
 
 # ---------------------------------------------------------------------------- launches
 BLOCK = 256
+VALUES_BLOCK = 512      # kValuesBlock: attention_values workgroup (one per (b, h))
+GREEDY_CHUNK = 4096     # kGreedyChunk: logits per greedy workgroup
 
 
 def _cdiv(a: int, b: int) -> int:
@@ -261,9 +263,14 @@ def _rms_apply(shapes, consts, ext):
 # the 256 CUs; but every cross-workgroup split adds a coherent write/read round trip, and one
 # front sweeping the weight rows in address order streams best. Hence: J = 4 (512 B of each
 # weight row per wave) once O alone yields >= 250 tiles, else J = 1, and a split only up to
-# ~256 workgroups with >= 512-row slices.
+# ~256 workgroups with >= 512-row slices. The vector path (B <= 16, latency-bound) runs one
+# workgroup per (64-column tile, batch row) whose up to 16 waves take 64 reduction rows each, all
+# loaded in one round trip; it splits only beyond 1024 rows.
 LINEAR_TARGET_GROUPS = 256
+LINEAR_ZERO_PAGE = 256    # kZeroPage: leading workspace bytes that stay zero
 LINEAR_VECTOR_ROWS = 16
+LINEAR_VECTOR_WAVES = 16      # waves per vector-path workgroup at most (1024 threads)
+LINEAR_VECTOR_WAVE_ROWS = 64  # kVectorRows: reduction rows per wave
 
 
 def linear_tiling(b: int, i: int, o: int) -> dict:
@@ -276,20 +283,24 @@ def linear_tiling(b: int, i: int, o: int) -> dict:
         rows, row_tiles = _cdiv(b, 32) * 32, _cdiv(b, 32)
         shared = 3 * j * 16 * 64 * 4
         entry = f"ckl_linear_mfma{j}"
+        block = BLOCK
     elif b <= LINEAR_VECTOR_ROWS:
         tiles = _cdiv(o, 64)
-        chunk = min(_cdiv(i, 4) * 4, 128)
-        split = _cdiv(i, chunk)
-        rows, row_tiles = b, 1
-        shared = (b * chunk + 3 * b * 64) * 4
-        entry = "ckl_linear"
+        waves = min(LINEAR_VECTOR_WAVES, _cdiv(i, LINEAR_VECTOR_WAVE_ROWS))
+        chunk = LINEAR_VECTOR_WAVE_ROWS                   # rows per wave (kVectorRows)
+        split = _cdiv(i, waves * chunk)
+        rows, row_tiles = b, b                            # one workgroup per batch row
+        shared = 0
+        entry = "ckl_linear_rowvec"
+        block = 64 * waves
     else:
         return None
-    workspace = 256
+    workspace = LINEAR_ZERO_PAGE
     if split > 1:
-        workspace = _cdiv(4 * row_tiles * tiles, 256) * 256 + 4 * split * rows * o
+        counters = row_tiles * tiles if entry != "ckl_linear_rowvec" else b * tiles
+        workspace += _cdiv(4 * counters, 256) * 256 + 4 * split * rows * o
     return dict(grid=row_tiles * split * tiles, tiles=tiles, split=split, chunk=chunk, shared=shared, entry=entry,
-                workspace=workspace)
+                workspace=workspace, block=block)
 
 
 def _linear(shapes, consts, ext):
@@ -300,8 +311,8 @@ def _linear(shapes, consts, ext):
     t = linear_tiling(b, i, o)
     if t is None:
         return None
-    return Launch(t["grid"], (b, i, o, layer, t["tiles"], t["split"], t["chunk"], 0), shared=t["shared"],
-                  entry=t["entry"], workspace=t["workspace"])
+    return Launch(t["grid"], (b, i, o, layer, t["tiles"], t["split"], t["chunk"], 0), block=t["block"],
+                  shared=t["shared"], entry=t["entry"], workspace=t["workspace"])
 
 
 def _rope(shapes, consts, ext):
@@ -334,7 +345,8 @@ def _softmax(shapes, consts, ext):
     b, a, t = shapes[0]
     if not (ext[0] >= b and ext[1:] == (a, 1)):
         return None
-    return Launch(_cdiv(b * a, 4), (b, a, t))
+    row_threads = 64 if t <= 512 else 256           # one wave per row, or the whole workgroup
+    return Launch(_cdiv(b * a, BLOCK // row_threads), (b, a, t, row_threads))
 
 
 def _values(shapes, consts, ext):
@@ -342,7 +354,13 @@ def _values(shapes, consts, ext):
     layer = consts[4]
     if a * d != c or not (0 <= layer < l) or not (ext[0] >= d and ext[1:] == (a, b)):
         return None
-    return Launch(b * a, (l, b, a, t, d, layer))
+    # Enough row groups to keep ~8 rows in flight per lane over the whole capacity, at least one
+    # wave, at most VALUES_BLOCK threads; the D/4 lanes of a row must divide a wave.
+    width = d // 4 if d % 4 == 0 and d <= 256 and 64 % (d // 4) == 0 else 64
+    block = 64
+    while block < VALUES_BLOCK and (block // width) * 8 < t:
+        block *= 2
+    return Launch(b * a, (l, b, a, t, d, layer), block=block)
 
 
 def _binary(shapes, consts, ext):
@@ -357,7 +375,11 @@ def _unary(shapes, consts, ext):
 
 def _greedy(shapes, consts, ext):
     (b, v), (t, _b) = shapes[0], shapes[2]
-    return Launch(b, (b, v, t)) if ext[0] >= b and ext[1:] == (1, 1) else None
+    if not (ext[0] >= b and ext[1:] == (1, 1)):
+        return None
+    chunks = _cdiv(v, GREEDY_CHUNK)
+    workspace = 256 if chunks == 1 else _cdiv(12 * b, 256) * 256
+    return Launch(b * chunks, (b, v, t, chunks), workspace=workspace)
 
 
 def _advance(shapes, consts, ext):
