@@ -176,8 +176,9 @@ class CompiledProgram(_ContextManager):
             if not text.startswith("module {"):
                 raise ValueError("unexpected IR module header")
             text = "module attributes {" + attribute + "} {" + text[len("module {"):]
-        elif not identity:
-            self.selections = {}
+        elif self.selections:
+            raise RuntimeError("the gfx950 kernel library code object (ckl_kernels_gfx950.hsaco, or "
+                               "CKL_KERNEL_LIBRARY) is missing; build it with composable-kernel-language_amd/build.py")
         lib = _native.native()
         options = _native.CompileOptions(int(reuse_storage), int(fuse_pointwise), 1, target.chip.encode())
         handle = ctypes.c_void_p()

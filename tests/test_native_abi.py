@@ -32,6 +32,21 @@ def test_kernel_library_is_present():
     assert _native.library_identity().startswith("ckl.hip.library.")
 
 
+def test_missing_kernel_library_fails_loudly(tmp_path):
+    """Library-selected kernels never fall back silently when the gfx950 code object is absent."""
+    import os
+    import subprocess
+    import sys
+    root = Path(__file__).resolve().parents[1]
+    code = ("import sys; sys.path[:0] = ['composable-kernel-language_amd/python', 'composable-kernel-language_amd']\n"
+            "from programs import vector_pipeline as vp\n"
+            "try:\n    vp.lower(1024).compile(fuse_pointwise=False)\nexcept RuntimeError as e:\n"
+            "    print('raised', e)\n")
+    env = dict(os.environ, CKL_KERNEL_LIBRARY=str(tmp_path / "absent.hsaco"))
+    out = subprocess.run([sys.executable, "-c", code], cwd=root, env=env, capture_output=True, text=True, timeout=120)
+    assert "raised" in out.stdout and "kernel library" in out.stdout, out.stdout + out.stderr
+
+
 def test_errors_map_to_python_exceptions():
     with pytest.raises(RuntimeError, match="unknown pass"):
         _native.native_opt("module {\n}\n", ["no-such-pass"])
