@@ -969,7 +969,8 @@ std::string canonicalFunction(const Op &function) {
 // ================================================================ clone
 namespace {
 struct Cloner {
-  std::unordered_map<const Value *, Value *> map;
+  ValueMap own;
+  ValueMap &map = own;
 
   std::unique_ptr<Op> op(const Op &src, Block *parent) {
     auto out = std::make_unique<Op>();
@@ -1017,6 +1018,11 @@ std::unique_ptr<Module> cloneModule(const Module &module) {
   auto out = std::make_unique<Module>();
   out->op = c.op(*module.op, nullptr);
   return out;
+}
+
+std::unique_ptr<Op> cloneOp(const Op &op, Block *parent, ValueMap &map) {
+  Cloner c{{}, map};
+  return c.op(op, parent);
 }
 
 } // namespace ckl

@@ -14,6 +14,7 @@
 #include <optional>
 #include <stdexcept>
 #include <string>
+#include <unordered_map>
 #include <vector>
 
 namespace ckl {
@@ -149,6 +150,10 @@ std::string canonicalFunction(const Op &function);
 
 // Deep copy (values remapped).
 std::unique_ptr<Module> cloneModule(const Module &module);
+// Copy of `op` (with its regions) owned by `parent`: operands found in `map` are replaced, and
+// the copies of results and block arguments are recorded in `map`.
+using ValueMap = std::unordered_map<const Value *, Value *>;
+std::unique_ptr<Op> cloneOp(const Op &op, Block *parent, ValueMap &map);
 
 // Walk helpers.
 void walkPreOrder(Op *op, const std::function<void(Op *)> &fn);
