@@ -87,11 +87,11 @@ def decoder_node_bytes(c, position):
 LIGHT_RESET = ("tokens", "position", "history", "logits")
 
 
-def time_variants(session, c, samples, warmup, log_prefix):
+def time_variants(session, c, samples, warmup, log_prefix, only=None):
     """Timing resets restore the small mutable state only: every run rewrites the cache rows it
     reads (positions >= the prefill position) before reading them, with deterministic kernels."""
     state = session.state
-    rows = variants(c.steps)
+    rows = [row for row in variants(c.steps) if not only or row[0] in only]
     metrics = {name: [] for name, *_ in rows}
     setup = {}
     for name, reuse, mode, group in rows:
@@ -130,31 +130,37 @@ def run_config(name, c, args, device):
     arrays, prompts = synthetic_inputs(c, args.seed, init="baseline")
     session = DecoderSession(c, device, arrays=arrays)
     t1 = time.time()
-    session.prefill(prompts, progress=lambda done, total: log(f"[{name}] prefill {done}/{total}"))
+    session.prefill(prompts, mode="ordinary", progress=lambda done, total: log(f"[{name}] prefill {done}/{total}"))
     t2 = time.time()
     log(f"[{name}] inputs+compile+bind {t1 - t0:.1f}s, device prefill of {c.context - 1} steps {t2 - t1:.2f}s")
-    table = time_variants(session, c, args.samples, args.warmup, f"[{name}]")
+    table = time_variants(session, c, args.samples, args.warmup, f"[{name}]", args.variants)
     heap = {}
     for reuse, program in session.programs.items():
         heap[str(reuse)] = sum(int(line.split("bytes = ")[1].split(" ")[0]) for line in program.executable_ir.splitlines()
                                if '"ckl_exec.heap"' in line)
     # State after one timed generation (the checker compares it with the CPU oracle).
     session.state.reset()
-    session.invocations[True].run(mode="graph", batch_size=c.steps)
+    session.invocations[True].run(mode="graph" if "batched_inferred" in table else "ordinary", batch_size=c.steps)
     final = {k: session.state.download(k) for k in ("tokens", "history", "position", "logits")}
-    inferred, capture = table["inferred"]["median_us"], table["capture"]["median_us"]
+
+    def median(variant):
+        return table[variant]["median_us"] if variant in table else None
+
+    def ratio(slow, fast):
+        return median(slow) / median(fast) if median(slow) and median(fast) else None
+
     position = c.context - 1
     mean_bytes = statistics.mean(algorithmic_step_bytes(c, position + s) for s in range(c.steps))
-    step_us = table["batched_inferred"]["median_us"]
+    step_us = median("batched_inferred") or min(v["median_us"] for v in table.values())
     result = dict(config=vars(c), steps=c.steps, variants=table,
-                  inferred_us=inferred, capture_us=capture, ordinary_us=table["sequential"]["median_us"],
-                  inferred_over_capture=capture / inferred,
-                  inferred_reuse_over_capture_reuse=table["capture_reuse"]["median_us"] / table["inferred_reuse"]["median_us"],
+                  inferred_us=median("inferred"), capture_us=median("capture"), ordinary_us=median("sequential"),
+                  inferred_over_capture=ratio("capture", "inferred"),
+                  inferred_reuse_over_capture_reuse=ratio("capture_reuse", "inferred_reuse"),
                   scratch_bytes={"reuse_off": heap["False"], "reuse_on": heap["True"]},
                   tokens_per_s=c.batch * 1e6 / step_us,
                   algorithmic_bytes_per_step=mean_bytes,
                   step_hbm_fraction=mean_bytes / (step_us * 1e-6) / HBM_PEAK)
-    log(f"[{name}] inferred/capture speedup {result['inferred_over_capture']:.3f}x; scratch {heap['False']} -> {heap['True']} B; "
+    log(f"[{name}] inferred/capture speedup {result['inferred_over_capture']}; scratch {heap['False']} -> {heap['True']} B; "
         f"step roofline {result['step_hbm_fraction']:.3f} of 8 TB/s")
     return session, result, final
 
@@ -162,6 +168,16 @@ def run_config(name, c, args, device):
 def c_name(c):
     from programs.decoder_config import CONFIGS
     return next((k for k, v in CONFIGS.items() if (v.batch, v.hidden, v.layers, v.vocab) == (c.batch, c.hidden, c.layers, c.vocab)), None)
+
+
+def measured_traffic(config, family):
+    """HBM bytes per launch of `family` on `config` from the committed rocprofv3 FETCH_SIZE and
+    WRITE_SIZE passes (profiles/decoder_<config>_hbm_traffic.json, scaled by the copy-kernel
+    calibration); None when no such measurement exists."""
+    path = ROOT / "profiles" / f"decoder_{config}_hbm_traffic.json"
+    if not config or not path.exists():
+        return None
+    return json.loads(path.read_text()).get("families", {}).get(family)
 
 
 def kernel_roofline(session, c, iterations=10):
@@ -198,7 +214,7 @@ def kernel_roofline(session, c, iterations=10):
     per_launch = entry["algorithmic_bytes"] / entry["launches"]
     achieved = per_launch / (avg * 1e-6)
     roofline = {"bound": "hbm", "kernel": f"ckl_{dominant}", "achieved": achieved / 1e9, "peak": HBM_PEAK / 1e9,
-                "unit": "GB/s", "frac": achieved / HBM_PEAK, "traffic": None,
+                "unit": "GB/s", "frac": achieved / HBM_PEAK, "traffic": measured_traffic(c_name(c), dominant),
                 "algorithmic_bytes_per_launch": per_launch, "avg_launch_us": avg,
                 "config": c_name(c), "position": position}
     return summary, dominant, roofline
@@ -258,6 +274,9 @@ def main():
     parser.add_argument("--samples", type=int, default=7)
     parser.add_argument("--seed", type=int, default=123)
     parser.add_argument("--configs", nargs="+", default=["small", "wide", "deep", "large"])
+    parser.add_argument("--variants", nargs="+", default=None, choices=[v[0] for v in variants(16)],
+                        help="time only these variants (default: all); kernel timings and the roofline do "
+                             "not depend on the run mode")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--output", type=Path, default=None, help="also write the full JSON result here")
     args = parser.parse_args()
@@ -293,10 +312,11 @@ def main():
         del session
     vector = vector_pipeline(device, args.samples)
     head = headline or next(iter(configs.values()))
+    value = next(v for v in (head["inferred_us"], head["ordinary_us"], head["capture_us"]) if v is not None)
     large = configs.get("large", {})
     line = {
-        "metric": METRIC, "value": head["inferred_us"], "unit": "us/step", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": head["inferred_us"] / 1000.0, "higher_is_better": False,
+        "metric": METRIC, "value": value, "unit": "us/step", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": value / 1000.0, "higher_is_better": False,
         "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic (seeded N(0,0.02) weights, random prompts)",
         "config": {"workload": "small decoder (B8 C64 A4x16 L2 F256 V256, ctx 16, 16 greedy steps)",
                    "inferred_us": head["inferred_us"], "capture_us": head["capture_us"],
