@@ -1,0 +1,77 @@
+// Argument blocks of the gfx950 kernel library (library.hip), shared with the HIP executor.
+//
+// Every library kernel takes ONE of these structs by value. Its layout is the CKL kernel's
+// arguments in order (buffers as pointers, scalars by value) followed by the int32 shape
+// constants chosen by python/ckl/library.py and, for some families, the workspace pointer the
+// executor appends (ckl_workspace). The executor packs arguments with natural alignment and pads
+// the block to 8 bytes, which is the layout of these aligned(8) structs.
+//
+// Chain entry points (several dependent dispatches executed as one launch in the inferred graph)
+// take the member blocks back to back: struct { First first; Second second; ... }. Each member
+// is aligned(8) with a size that is a multiple of 8, so the executor concatenates the members'
+// packed blocks unchanged. The executor reads these structs (csrc/runtime/chains.cpp) to decide
+// whether a chain may run fused; the kernels read them to run it.
+#pragma once
+
+#include <stdint.h>
+
+#define CKL_ALIGN __attribute__((aligned(8)))
+
+namespace ckl::kernels {
+
+constexpr int kMaxGroup = 4;
+
+// Sibling-group entry points: up to kMaxGroup independent dispatches of one family in one grid;
+// member m owns logical blocks [start[m], start[m+1]).
+template <typename Args> struct CKL_ALIGN Group {
+  Args m[kMaxGroup];
+  int start[kMaxGroup + 1];
+  int count;
+};
+
+// dst[b, c] = table[tokens[b], c]   (workloads.py:33-39)
+struct CKL_ALIGN EmbeddingArgs { const int *tokens; const float *table; float *dst; int B, C, V; };
+// inv[b] = rsqrt(sum_c x[b,c]^2 / C + eps)   (workloads.py:42-49)
+struct CKL_ALIGN RmsStatsArgs { const float *x; float *inv; float eps; int B, C; };
+// dst[b, c] = x[b, c] * inv[b] * gain[layer, c]   (workloads.py:52-58)
+struct CKL_ALIGN RmsApplyArgs { const float *x; const float *inv; const float *gain; float *dst; int B, C, layer; };
+// dst[b, o] = sum_i x[b, i] * w[layer, i, o]   (workloads.py:61-69)
+struct CKL_ALIGN LinearArgs {
+  const float *x; const float *w; float *dst; int B, I, O, layer;
+  int tilesN, kSplit, kChunk, pad;
+  unsigned char *workspace;
+};
+// adjacent-pair rotation at the current position   (workloads.py:72-85)
+struct CKL_ALIGN RopeArgs { const float *src; const float *table; const int *position; float *dst; int B, A, R, T; };
+// kc/vc[layer, b, h, p, :] = k/v[b, h*D : h*D+D]   (workloads.py:88-97)
+struct CKL_ALIGN AppendArgs { const float *k; const float *v; float *kc; float *vc; const int *position; int L, B, A, T, D, layer; };
+// scores[b, h, t] = q . kc[layer, b, h, t] * scale   (workloads.py:100-111)
+struct CKL_ALIGN ScoresArgs { const float *q; const float *kc; const int *position; float *scores; float scale; int L, B, A, T, D, layer; };
+// probs[b, h, :] = softmax(scores[b, h, :p+1])   (workloads.py:114-128)
+struct CKL_ALIGN SoftmaxArgs { const float *scores; const int *position; float *probs; int B, A, T, rowThreads; };
+// dst[b, h*D+d] = sum_t probs[b, h, t] * vc[layer, b, h, t, d]   (workloads.py:131-142)
+struct CKL_ALIGN ValuesArgs { const float *probs; const float *vc; const int *position; float *dst; int L, B, A, T, D, layer; };
+// add / multiply / silu over n elements   (workloads.py:145-167)
+struct CKL_ALIGN BinaryArgs { const float *x; const float *y; float *dst; int n; };
+struct CKL_ALIGN UnaryArgs { const float *src; float *dst; int n; };
+// tokens[b] = history[p, b] = argmax logits[b, :]   (workloads.py:170-183)
+struct CKL_ALIGN GreedyArgs {
+  const float *logits; int *tokens; int *history; const int *position; int B, V, T, chunks;
+  unsigned char *workspace;
+};
+// position[0] += 1   (workloads.py:186-188)
+struct CKL_ALIGN AdvanceArgs { int *position; };
+// dst[i] = src[i] + bias   (examples/vector_pipeline.py:11-16)
+struct CKL_ALIGN UpdateArgs { const float *src; float *dst; float bias; int n; };
+
+// Chains (member blocks back to back, in dispatch order).
+struct CKL_ALIGN RmsChainArgs { RmsStatsArgs stats; RmsApplyArgs apply; };
+struct CKL_ALIGN AddRmsChainArgs { BinaryArgs add; RmsStatsArgs stats; RmsApplyArgs apply; };
+struct CKL_ALIGN EmbeddingRmsChainArgs { EmbeddingArgs embedding; RmsStatsArgs stats; RmsApplyArgs apply; };
+struct CKL_ALIGN SiluMultiplyChainArgs { UnaryArgs silu; BinaryArgs multiply; };
+struct CKL_ALIGN SoftmaxValuesChainArgs { SoftmaxArgs softmax; ValuesArgs values; };
+
+// Largest row (in floats) a softmax -> attention_values chain keeps in LDS.
+constexpr int kChainSoftmaxRow = 8192;
+
+} // namespace ckl::kernels

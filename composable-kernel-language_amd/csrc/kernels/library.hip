@@ -16,15 +16,11 @@
 
 #include <stdint.h>
 
-#define CKL_ALIGN __attribute__((aligned(8)))
-constexpr int kMaxGroup = 4;
-constexpr int kBlock = 256;
+#include "args.h"
 
-template <typename Args> struct CKL_ALIGN Group {
-  Args m[kMaxGroup];
-  int start[kMaxGroup + 1];
-  int count;
-};
+using namespace ckl::kernels;
+
+constexpr int kBlock = 256;
 
 #define CKL_ENTRY_ATTR(name, Args, body, threads, attributes)                                        \
   extern "C" __global__ __launch_bounds__(threads) attributes void ckl_##name(const Args a) { body(a, blockIdx.x); } \
@@ -100,7 +96,6 @@ __device__ __forceinline__ int load_position(const int *position) { return *posi
 
 // ------------------------------------------------------------------ embedding
 // dst[b, c] = table[tokens[b], c]   (workloads.py:33-39)
-struct CKL_ALIGN EmbeddingArgs { const int *tokens; const float *table; float *dst; int B, C, V; };
 __device__ void embedding_body(const EmbeddingArgs &a, int block) {
   long i = long(block) * kBlock + threadIdx.x;
   if ((a.C & 3) == 0) {
@@ -121,8 +116,18 @@ __device__ void embedding_body(const EmbeddingArgs &a, int block) {
 CKL_ENTRY(embedding, EmbeddingArgs, embedding_body)
 
 // ------------------------------------------------------------------ rms_stats
-// inv[b] = rsqrt(sum_c x[b,c]^2 / C + eps)   (workloads.py:42-49); one wave per row.
-struct CKL_ALIGN RmsStatsArgs { const float *x; float *inv; float eps; int B, C; };
+// inv[b] = rsqrt(sum_c x[b,c]^2 / C + eps)   (workloads.py:42-49); one wave per row. The squares
+// are accumulated with explicit FMAs, so the row chains below (which compute the same row sums
+// from the values they produce) round exactly as this kernel does.
+__device__ __forceinline__ float add_squares(float total, float4 v) {
+  total = __builtin_fmaf(v.x, v.x, total);
+  total = __builtin_fmaf(v.y, v.y, total);
+  total = __builtin_fmaf(v.z, v.z, total);
+  return __builtin_fmaf(v.w, v.w, total);
+}
+__device__ __forceinline__ float rms_inverse(float total, int C, float eps) {
+  return 1.0f / __fsqrt_rn(total / float(C) + eps);
+}
 __device__ void rms_stats_body(const RmsStatsArgs &a, int block) {
   int lane = threadIdx.x & 63;
   int row = block * (kBlock / 64) + (threadIdx.x >> 6);
@@ -131,21 +136,20 @@ __device__ void rms_stats_body(const RmsStatsArgs &a, int block) {
   float total = 0.f;
   if ((a.C & 3) == 0) {
     const float4 *x4 = reinterpret_cast<const float4 *>(x);
-    for (int c = lane; c < a.C / 4; c += 64) {
-      float4 v = x4[c];
-      total += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-    }
+    for (int c = lane; c < a.C / 4; c += 64) total = add_squares(total, x4[c]);
   } else {
-    for (int c = lane; c < a.C; c += 64) total += x[c] * x[c];
+    for (int c = lane; c < a.C; c += 64) total = __builtin_fmaf(x[c], x[c], total);
   }
   total = wave_sum(total);
-  if (lane == 0) a.inv[row] = 1.0f / __fsqrt_rn(total / float(a.C) + a.eps);
+  if (lane == 0) a.inv[row] = rms_inverse(total, a.C, a.eps);
 }
 CKL_ENTRY(rms_stats, RmsStatsArgs, rms_stats_body)
 
 // ------------------------------------------------------------------ rms_apply
 // dst[b, c] = x[b, c] * inv[b] * gain[layer, c]   (workloads.py:52-58)
-struct CKL_ALIGN RmsApplyArgs { const float *x; const float *inv; const float *gain; float *dst; int B, C, layer; };
+__device__ __forceinline__ float4 rms_scale(float4 x, float s, float4 g) {
+  return make_float4(x.x * s * g.x, x.y * s * g.y, x.z * s * g.z, x.w * s * g.w);
+}
 __device__ void rms_apply_body(const RmsApplyArgs &a, int block) {
   long i = long(block) * kBlock + threadIdx.x;
   const float *gain = a.gain + long(a.layer) * a.C;
@@ -156,7 +160,7 @@ __device__ void rms_apply_body(const RmsApplyArgs &a, int block) {
     float s = a.inv[b];
     float4 x = reinterpret_cast<const float4 *>(a.x + long(b) * a.C)[c4];
     float4 g = reinterpret_cast<const float4 *>(gain)[c4];
-    reinterpret_cast<float4 *>(a.dst + long(b) * a.C)[c4] = make_float4(x.x * s * g.x, x.y * s * g.y, x.z * s * g.z, x.w * s * g.w);
+    reinterpret_cast<float4 *>(a.dst + long(b) * a.C)[c4] = rms_scale(x, s, g);
   } else {
     if (i >= long(a.B) * a.C) return;
     int b = int(i / a.C), c = int(i % a.C);
@@ -164,6 +168,104 @@ __device__ void rms_apply_body(const RmsApplyArgs &a, int block) {
   }
 }
 CKL_ENTRY(rms_apply, RmsApplyArgs, rms_apply_body)
+
+// ------------------------------------------------------------------ row chains ending in rms
+// [producer ->] rms_stats -> rms_apply as one launch of rms_stats's geometry (one wave per row):
+// the wave produces its row (embedding gather or residual add, written to the producer's dst),
+// sums the squares of the values it produced, writes inv[row] (unless the executor cleared the
+// pointer because nothing outside the chain reads inv), then scales the row. Each lane
+// touches the same elements in every phase, so it only reads back its own writes. The executor
+// runs a chain only when its buffers are pairwise disjoint or identical (csrc/runtime/chains.cpp).
+// Per element the arithmetic is that of the separate kernels, so results are bit-identical.
+__device__ __forceinline__ void rms_finish_row(const RmsStatsArgs &stats, const RmsApplyArgs &apply, int row,
+                                               float total, int lane) {
+  total = wave_sum(total);
+  const float s = rms_inverse(total, stats.C, stats.eps);
+  if (lane == 0 && stats.inv) stats.inv[row] = s;   // null: only the chain reads inv
+  const int C = apply.C;
+  const float *gain = apply.gain + long(apply.layer) * C;
+  const float *x = apply.x + long(row) * C;
+  float *dst = apply.dst + long(row) * C;
+  if ((C & 3) == 0) {
+    for (int c = lane; c < C / 4; c += 64)
+      reinterpret_cast<float4 *>(dst)[c] = rms_scale(reinterpret_cast<const float4 *>(x)[c], s,
+                                                     reinterpret_cast<const float4 *>(gain)[c]);
+  } else {
+    for (int c = lane; c < C; c += 64) dst[c] = x[c] * s * gain[c];
+  }
+}
+
+__device__ void rms_stats__rms_apply_body(const RmsChainArgs &a, int block) {
+  const int lane = threadIdx.x & 63;
+  const int row = block * (kBlock / 64) + (threadIdx.x >> 6);
+  if (row >= a.stats.B) return;
+  const int C = a.stats.C;
+  const float *x = a.stats.x + long(row) * C;
+  float total = 0.f;
+  if ((C & 3) == 0) {
+    for (int c = lane; c < C / 4; c += 64) total = add_squares(total, reinterpret_cast<const float4 *>(x)[c]);
+  } else {
+    for (int c = lane; c < C; c += 64) total = __builtin_fmaf(x[c], x[c], total);
+  }
+  rms_finish_row(a.stats, a.apply, row, total, lane);
+}
+CKL_ENTRY(rms_stats__rms_apply, RmsChainArgs, rms_stats__rms_apply_body)
+
+__device__ void add__rms_stats__rms_apply_body(const AddRmsChainArgs &a, int block) {
+  const int lane = threadIdx.x & 63;
+  const int row = block * (kBlock / 64) + (threadIdx.x >> 6);
+  if (row >= a.stats.B) return;
+  const int C = a.stats.C;
+  const long base = long(row) * C;
+  float total = 0.f;
+  if ((C & 3) == 0) {
+    const float4 *x = reinterpret_cast<const float4 *>(a.add.x + base), *y = reinterpret_cast<const float4 *>(a.add.y + base);
+    float4 *dst = reinterpret_cast<float4 *>(a.add.dst + base);
+    for (int c = lane; c < C / 4; c += 64) {
+      float4 u = x[c], w = y[c];
+      float4 v = make_float4(u.x + w.x, u.y + w.y, u.z + w.z, u.w + w.w);
+      dst[c] = v;
+      total = add_squares(total, v);
+    }
+  } else {
+    for (int c = lane; c < C; c += 64) {
+      float v = a.add.x[base + c] + a.add.y[base + c];
+      a.add.dst[base + c] = v;
+      total = __builtin_fmaf(v, v, total);
+    }
+  }
+  rms_finish_row(a.stats, a.apply, row, total, lane);
+}
+CKL_ENTRY(add__rms_stats__rms_apply, AddRmsChainArgs, add__rms_stats__rms_apply_body)
+
+__device__ void embedding__rms_stats__rms_apply_body(const EmbeddingRmsChainArgs &a, int block) {
+  const int lane = threadIdx.x & 63;
+  const int row = block * (kBlock / 64) + (threadIdx.x >> 6);
+  if (row >= a.stats.B) return;
+  const EmbeddingArgs &e = a.embedding;
+  const int C = e.C;
+  const int token = e.tokens[row];
+  const bool valid = token >= 0 && token < e.V;
+  const float nan = __builtin_nanf("");
+  float total = 0.f;
+  if ((C & 3) == 0) {
+    const float4 *table = reinterpret_cast<const float4 *>(e.table + long(valid ? token : 0) * C);
+    float4 *dst = reinterpret_cast<float4 *>(e.dst + long(row) * C);
+    for (int c = lane; c < C / 4; c += 64) {
+      float4 v = valid ? table[c] : make_float4(nan, nan, nan, nan);
+      dst[c] = v;
+      total = add_squares(total, v);
+    }
+  } else {
+    for (int c = lane; c < C; c += 64) {
+      float v = valid ? e.table[long(token) * C + c] : nan;
+      e.dst[long(row) * C + c] = v;
+      total = __builtin_fmaf(v, v, total);
+    }
+  }
+  rms_finish_row(a.stats, a.apply, row, total, lane);
+}
+CKL_ENTRY(embedding__rms_stats__rms_apply, EmbeddingRmsChainArgs, embedding__rms_stats__rms_apply_body)
 
 // ------------------------------------------------------------------ linear
 // dst[b, o] = sum_i x[b, i] * w[layer, i, o]   (workloads.py:61-69)
@@ -174,10 +276,11 @@ CKL_ENTRY(rms_apply, RmsApplyArgs, rms_apply_body)
 // [kg*kChunk, (kg+1)*kChunk), which its 4 waves share.
 //   ckl_linear_rowvec (vector, B <= 16): one batch row and 64 output columns (lane <-> column)
 //           per workgroup, the reduction split over its waves;
-//   ckl_linear_mfma1/4 (f32 MFMA, B > 16): v_mfma_f32_32x32x2f32 over 32 batch rows; each lane loads
-//           J = 1 / 4 consecutive weight columns with one vector load, and MFMA j accumulates
-//           columns {J*c + j}, so one wave owns a 32 x 32J tile. The K index is permuted so the
-//           A operand (x) is one float4 load per 8 reduction rows.
+//   ckl_linear_mfma<J>x<S> (f32 MFMA, B > 16): v_mfma_f32_32x32x2f32 over 32 batch rows; each lane
+//           loads J = 1, 2 or 4 consecutive weight columns with one vector load, and MFMA j
+//           accumulates columns {J*c + j}, so one wave owns a 32 x 32J tile; a wave streams
+//           16*S reduction rows per stage. The K index is permuted so the A operand (x) is one
+//           float4 load per 8 reduction rows.
 // Partial tiles of the 4 waves are added through LDS in wave order. With kSplit > 1 every
 // workgroup writes its partial tile to the workspace with agent-coherent stores and bumps the
 // tile's completion counter; the last one to arrive adds the kSplit partials in kg order,
@@ -185,11 +288,6 @@ CKL_ENTRY(rms_apply, RmsApplyArgs, rms_apply_body)
 //
 // workspace layout: counters (rowTiles*tilesN uint32, padded to 256 B), then partial tiles
 // float[kSplit][rowTiles*rowsPerTile][O] (rowsPerTile = 32 for MFMA, B for the vector path).
-struct CKL_ALIGN LinearArgs {
-  const float *x; const float *w; float *dst; int B, I, O, layer;
-  int tilesN, kSplit, kChunk, pad;
-  unsigned char *workspace;
-};
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 // s_waitcnt immediate (gfx9 encoding) that waits for vmcnt == 0 only: outstanding vector memory
@@ -272,21 +370,21 @@ template <int J> __device__ __forceinline__ void load_columns(float (&out)[J], c
   }
 }
 
-// 16 reduction rows of one lane (two 8-row super-steps): x[row][k+8u .. k+8u+3] and the lane's
-// J weight columns of rows k+8u+i. Full stages load without predicates or selects, so the next
-// stage's loads stay in flight under the current stage's MFMAs: a batch row >= B (x row clamped
-// to 0) only feeds output row >= B and a column >= O (clamped to column 0) only feeds output
-// column >= O, neither of which is stored. The tail stage zeroes reduction rows past k1 (their
-// addresses are clamped to row k1-1).
-template <int J> struct MfmaStage {
-  float x[2][4];
-  float w[2][4][J];
+// One stage = 16*S reduction rows of one lane (2S 8-row super-steps): x[row][k+8u .. k+8u+3] and
+// the lane's J weight columns of rows k+8u+i. Full stages load without predicates or selects, so
+// the next stage's loads stay in flight under the current stage's MFMAs: a batch row >= B (x row
+// clamped to 0) only feeds output row >= B and a column >= O (clamped to column 0) only feeds
+// output column >= O, neither of which is stored. Tail stages (S = 1) zero reduction rows past k1
+// (their addresses are clamped to row k1-1).
+template <int J, int S> struct MfmaStage {
+  float x[2 * S][4];
+  float w[2 * S][4][J];
 };
 
-template <int J, bool Tail>
-__device__ __forceinline__ void mfma_load(MfmaStage<J> &st, const float *xr, const float *w, long O, int k, int k1) {
+template <int J, int S, bool Tail>
+__device__ __forceinline__ void mfma_load(MfmaStage<J, S> &st, const float *xr, const float *w, long O, int k, int k1) {
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
+  for (int u = 0; u < 2 * S; ++u) {
     const int kk = k + 8 * u;
     if constexpr (!Tail) {
       float4 v = *reinterpret_cast<const float4 *>(xr + kk);
@@ -309,16 +407,16 @@ __device__ __forceinline__ void mfma_load(MfmaStage<J> &st, const float *xr, con
   }
 }
 
-template <int J> __device__ __forceinline__ void mfma_compute(const MfmaStage<J> &st, floatx16 (&acc)[J]) {
+template <int J, int S> __device__ __forceinline__ void mfma_compute(const MfmaStage<J, S> &st, floatx16 (&acc)[J]) {
 #pragma unroll
-  for (int u = 0; u < 2; ++u)
+  for (int u = 0; u < 2 * S; ++u)
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int j = 0; j < J; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(st.x[u][i], st.w[u][i][j], acc[j], 0, 0, 0);
 }
 
-template <int J> __device__ void linear_mfma(const LinearArgs &a, int block, float *smem) {
+template <int J, int S> __device__ void linear_mfma(const LinearArgs &a, int block, float *smem) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform: scalar loop control
   const int m = lane & 31, s = lane >> 5;
@@ -338,34 +436,40 @@ template <int J> __device__ void linear_mfma(const LinearArgs &a, int block, flo
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[j][r] = 0.f;
 
-  // The slice is cut into 16-row stages dealt round-robin to the 4 waves (wave w takes stages
+  // The slice is cut into 16*S-row stages dealt round-robin to the 4 waves (wave w takes stages
   // w, w+4, ...), so the waves of a workgroup stream neighbouring weight rows at any moment.
   // Full stages are double-buffered: stage u+1's loads are in flight while stage u feeds the
-  // MFMAs. The loop body has no conditional loads (the compiler would sink them into the
-  // condition and drain the load queue at the join); with an even stage count the last prefetch
-  // re-reads the last stage, an L2 hit. sched_barrier keeps each stage's loads issued as one
-  // group ahead of the other stage's MFMAs. A ragged last stage is handled by its owner.
-  const int fullTotal = (kb1 - kb0) / 16;
+  // MFMAs (S sets how many bytes each wave keeps in flight). The loop body has no conditional
+  // loads (the compiler would sink them into the condition and drain the load queue at the join);
+  // with an even stage count the last prefetch re-reads the last stage, an L2 hit. sched_barrier
+  // keeps each stage's loads issued as one group ahead of the other stage's MFMAs. The ragged
+  // rest of the slice is cut into 16-row tail stages, dealt round-robin after the full ones.
+  constexpr int R = 16 * S;
+  const int fullTotal = (kb1 - kb0) / R;
   const int full = fullTotal > wave ? (fullTotal - wave + 3) / 4 : 0;
-  const int k = kb0 + 16 * wave + 4 * s;               // this lane's row in the wave's first stage
+  const int k = kb0 + R * wave + 4 * s;                // this lane's row in the wave's first stage
   const int k1 = kb1;
-  MfmaStage<J> sa, sb;
+  MfmaStage<J, S> sa, sb;
   int t = 0;
-  if (full > 0) mfma_load<J, false>(sa, xr, w, a.O, k, k1);
+  if (full > 0) mfma_load<J, S, false>(sa, xr, w, a.O, k, k1);
   for (; t + 1 < full; t += 2) {
-    mfma_load<J, false>(sb, xr, w, a.O, k + 64 * (t + 1), k1);
+    mfma_load<J, S, false>(sb, xr, w, a.O, k + 4 * R * (t + 1), k1);
     __builtin_amdgcn_sched_barrier(0);
-    mfma_compute<J>(sa, acc);
+    mfma_compute<J, S>(sa, acc);
     __builtin_amdgcn_sched_barrier(0);
-    mfma_load<J, false>(sa, xr, w, a.O, k + 64 * min(t + 2, full - 1), k1);
+    mfma_load<J, S, false>(sa, xr, w, a.O, k + 4 * R * min(t + 2, full - 1), k1);
     __builtin_amdgcn_sched_barrier(0);
-    mfma_compute<J>(sb, acc);
+    mfma_compute<J, S>(sb, acc);
     __builtin_amdgcn_sched_barrier(0);
   }
-  if (t < full) mfma_compute<J>(sa, acc);
-  if (kb0 + 16 * fullTotal < kb1 && fullTotal % 4 == wave) {
-    mfma_load<J, true>(sa, xr, w, a.O, kb0 + 16 * fullTotal + 4 * s, k1);
-    mfma_compute<J>(sa, acc);
+  if (t < full) mfma_compute<J, S>(sa, acc);
+  const int tailBase = kb0 + R * fullTotal;
+  const int tailStages = (kb1 - tailBase + 15) / 16;
+#pragma unroll 1
+  for (int q = (wave - fullTotal % 4 + 4) % 4; q < tailStages; q += 4) {
+    MfmaStage<J, 1> st;
+    mfma_load<J, 1, true>(st, xr, w, a.O, tailBase + 16 * q + 4 * s, k1);
+    mfma_compute<J, 1>(st, acc);
   }
 
   // Waves 1..3 hand their tiles to wave 0 through LDS; wave 0 adds them in wave order.
@@ -463,22 +567,24 @@ __device__ void linear_rowvec_body(const LinearArgs &a, int block) {
     split_finish(a, split_partials(a, a.B * a.tilesN), long(a.B) * a.O, b, 1, tn * 64, 64);
 }
 
-__device__ void linear_mfma1_body(const LinearArgs &a, int block) {
+template <int J, int S> __device__ void linear_mfma_body(const LinearArgs &a, int block) {
   extern __shared__ float smem[];
-  linear_mfma<1>(a, block, smem);
-}
-__device__ void linear_mfma4_body(const LinearArgs &a, int block) {
-  extern __shared__ float smem[];
-  linear_mfma<4>(a, block, smem);
+  linear_mfma<J, S>(a, block, smem);
 }
 CKL_ENTRY_ATTR(linear_rowvec, LinearArgs, linear_rowvec_body, 1024, )
-CKL_ENTRY(linear_mfma1, LinearArgs, linear_mfma1_body)
-CKL_ENTRY_ATTR(linear_mfma4, LinearArgs, linear_mfma4_body, kBlock, CKL_TWO_WAVES)
+// ckl_linear_mfma<J>x<S>: J weight columns per lane, 16*S reduction rows per stage.
+CKL_ENTRY(linear_mfma1x1, LinearArgs, (linear_mfma_body<1, 1>))
+CKL_ENTRY(linear_mfma1x2, LinearArgs, (linear_mfma_body<1, 2>))
+CKL_ENTRY_ATTR(linear_mfma1x4, LinearArgs, (linear_mfma_body<1, 4>), kBlock, CKL_TWO_WAVES)
+CKL_ENTRY(linear_mfma2x1, LinearArgs, (linear_mfma_body<2, 1>))
+CKL_ENTRY_ATTR(linear_mfma2x2, LinearArgs, (linear_mfma_body<2, 2>), kBlock, CKL_TWO_WAVES)
+CKL_ENTRY_ATTR(linear_mfma2x4, LinearArgs, (linear_mfma_body<2, 4>), kBlock, CKL_TWO_WAVES)
+CKL_ENTRY_ATTR(linear_mfma4x1, LinearArgs, (linear_mfma_body<4, 1>), kBlock, CKL_TWO_WAVES)
+CKL_ENTRY_ATTR(linear_mfma4x2, LinearArgs, (linear_mfma_body<4, 2>), kBlock, CKL_TWO_WAVES)
 
 // ------------------------------------------------------------------ rope
 // Adjacent-pair rotation at position p (workloads.py:72-85):
 //   dst[b,c] = s[b,c]*cos - s[b,c+1]*sin; dst[b,c+1] = s[b,c]*sin + s[b,c+1]*cos, c = h*2R + 2r.
-struct CKL_ALIGN RopeArgs { const float *src; const float *table; const int *position; float *dst; int B, A, R, T; };
 __device__ void rope_body(const RopeArgs &a, int block) {
   long i = long(block) * kBlock + threadIdx.x;
   long pairs = long(a.B) * a.A * a.R;
@@ -497,7 +603,6 @@ CKL_ENTRY(rope, RopeArgs, rope_body)
 
 // ------------------------------------------------------------------ append_kv
 // kc[layer,b,h,p,d] = k[b,h*D+d]; vc[...] = v[...]   (workloads.py:88-97)
-struct CKL_ALIGN AppendArgs { const float *k; const float *v; float *kc; float *vc; const int *position; int L, B, A, T, D, layer; };
 __device__ void append_kv_body(const AppendArgs &a, int block) {
   long i = long(block) * kBlock + threadIdx.x;
   int p = load_position(a.position);
@@ -528,7 +633,6 @@ CKL_ENTRY(append_kv, AppendArgs, append_kv_body)
 // Groups of D/4 lanes hold one row as float4s; a wave issues kScoreBatch row loads per lane before
 // reducing any of them, so ~kScoreBatch KB per wave are in flight. Row addresses past the end
 // re-read an early row of the wave and their results are dropped (the loads stay unpredicated).
-struct CKL_ALIGN ScoresArgs { const float *q; const float *kc; const int *position; float *scores; float scale; int L, B, A, T, D, layer; };
 constexpr int kScoreBatch = 8;
 __device__ void attention_scores_body(const ScoresArgs &a, int block) {
   int chunks = (a.T + kBlock - 1) / kBlock;
@@ -580,12 +684,13 @@ CKL_ENTRY(attention_scores, ScoresArgs, attention_scores_body)
 // probs[b,h,t] = exp(s[t] - max) / sum_t' exp(s[t'] - max) over t <= p (workloads.py:114-128).
 // `rowThreads` (64 or 256) lanes per (b, h) row; each lane keeps up to kSoftmaxPerLane scores in
 // registers (one read of the row, one write), longer rows stream three passes.
-struct CKL_ALIGN SoftmaxArgs { const float *scores; const int *position; float *probs; int B, A, T, rowThreads; };
 constexpr int kSoftmaxPerLane = 8;
+constexpr int kValuesBlock = 512;
 
-// Reduction over the `rowThreads` lanes of one row (a wave, or the whole 4-wave workgroup).
+// Reduction over the `rowThreads` lanes of one row (a wave, or waves 0-3 of the workgroup). With
+// rowThreads > 64 every thread of the workgroup must call it (it synchronizes the workgroup).
 template <bool IsMax> __device__ __forceinline__ float row_reduce(float v, int rowThreads) {
-  __shared__ float across[kBlock / 64];
+  __shared__ float across[kValuesBlock / 64];
   v = IsMax ? wave_max(v) : wave_sum(v);
   if (rowThreads <= 64) return v;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -597,16 +702,15 @@ template <bool IsMax> __device__ __forceinline__ float row_reduce(float v, int r
   return r;
 }
 
-__device__ void softmax_body(const SoftmaxArgs &a, int block) {
-  const int rowsPerBlock = kBlock / a.rowThreads;
-  const int local = threadIdx.x % a.rowThreads;
-  long row = long(block) * rowsPerBlock + threadIdx.x / a.rowThreads;
-  const bool active = row < long(a.B) * a.A;       // uniform per row group (rowThreads divides kBlock)
+// Softmax of row `row` by the lanes with local index `local` < rowThreads (inactive lanes only
+// take part in the synchronization). Probabilities go to a.probs and, when `stage` is given, to
+// stage[t] as well.
+__device__ __forceinline__ void softmax_row(const SoftmaxArgs &a, long row, int local, bool active, float *stage) {
   int p = load_position(a.position);
   int end = min(p + 1, a.T);
   if (p < 0) end = 0;
   const float *s = a.scores + (active ? row : 0) * a.T;
-  float *out = a.probs + (active ? row : 0) * a.T;
+  float *out = a.probs ? a.probs + (active ? row : 0) * a.T : nullptr;   // null in a chain: LDS only
   if (end <= a.rowThreads * kSoftmaxPerLane) {
     float v[kSoftmaxPerLane];
     float m = -__builtin_inff();
@@ -628,7 +732,11 @@ __device__ void softmax_body(const SoftmaxArgs &a, int block) {
 #pragma unroll
     for (int u = 0; u < kSoftmaxPerLane; ++u) {
       int t = local + u * a.rowThreads;
-      if (active && t < end) out[t] = v[u] / total;
+      if (active && t < end) {
+        float q = v[u] / total;
+        if (out) out[t] = q;
+        if (stage) stage[t] = q;
+      }
     }
   } else {
     float m = -__builtin_inff();
@@ -638,8 +746,20 @@ __device__ void softmax_body(const SoftmaxArgs &a, int block) {
     for (int t = local; t < end; t += a.rowThreads) total += active ? expf(s[t] - m) : 0.f;
     total = row_reduce<false>(total, a.rowThreads);
     for (int t = local; t < end; t += a.rowThreads)
-      if (active) out[t] = expf(s[t] - m) / total;
+      if (active) {
+        float q = expf(s[t] - m) / total;
+        if (out) out[t] = q;
+        if (stage) stage[t] = q;
+      }
   }
+}
+
+__device__ void softmax_body(const SoftmaxArgs &a, int block) {
+  const int rowsPerBlock = kBlock / a.rowThreads;
+  const int local = threadIdx.x % a.rowThreads;
+  long row = long(block) * rowsPerBlock + threadIdx.x / a.rowThreads;
+  const bool active = row < long(a.B) * a.A;       // uniform per row group (rowThreads divides kBlock)
+  softmax_row(a, row, local, active, nullptr);
 }
 CKL_ENTRY(softmax, SoftmaxArgs, softmax_body)
 
@@ -648,18 +768,14 @@ CKL_ENTRY(softmax, SoftmaxArgs, softmax_body)
 // One workgroup per (b, h) of blockDim.x <= kValuesBlock threads (a power of two, chosen from the
 // cache capacity): groups of D/4 lanes own the float4 column slices of one row, blockDim/(D/4)
 // row groups stride over t with kValuesBatch row loads per lane in flight; the partial float4
-// sums are combined by a fixed-order tree in LDS.
-struct CKL_ALIGN ValuesArgs { const float *probs; const float *vc; const int *position; float *dst; int L, B, A, T, D, layer; };
-constexpr int kValuesBlock = 512;
+// sums are combined by a fixed-order tree in LDS. `probs` is the (b, h) row of probabilities
+// (global memory, or LDS in the softmax chain).
 constexpr int kValuesBatch = 8;
-__device__ void attention_values_body(const ValuesArgs &a, int block) {
+__device__ __forceinline__ void attention_values_row(const ValuesArgs &a, long bh, const float *probs) {
   __shared__ float4 partial[kValuesBlock];
-  long bh = block;
-  if (bh >= long(a.B) * a.A) return;
   int p = load_position(a.position);
   int end = min(p + 1, a.T);
   if (p < 0) end = 0;
-  const float *probs = a.probs + bh * a.T;
   const float *values = a.vc + (long(a.layer) * a.B * a.A + bh) * long(a.T) * a.D;
   float *dst = a.dst + bh * a.D;
   if ((a.D & 3) == 0 && a.D <= 4 * 64 && (64 % (a.D / 4)) == 0) {
@@ -678,7 +794,10 @@ __device__ void attention_values_body(const ValuesArgs &a, int block) {
       }
 #pragma unroll
       for (int u = 0; u < kValuesBatch; ++u) {
-        acc.x += pr[u] * v[u].x; acc.y += pr[u] * v[u].y; acc.z += pr[u] * v[u].z; acc.w += pr[u] * v[u].w;
+        acc.x = __builtin_fmaf(pr[u], v[u].x, acc.x);
+        acc.y = __builtin_fmaf(pr[u], v[u].y, acc.y);
+        acc.z = __builtin_fmaf(pr[u], v[u].z, acc.z);
+        acc.w = __builtin_fmaf(pr[u], v[u].w, acc.w);
       }
     }
     partial[threadIdx.x] = acc;
@@ -695,17 +814,37 @@ __device__ void attention_values_body(const ValuesArgs &a, int block) {
   } else {
     for (int d = threadIdx.x; d < a.D; d += blockDim.x) {
       float acc = 0.f;
-      for (int t = 0; t < end; ++t) acc += probs[t] * values[long(t) * a.D + d];
+      for (int t = 0; t < end; ++t) acc = __builtin_fmaf(probs[t], values[long(t) * a.D + d], acc);
       dst[d] = acc;
     }
   }
 }
+
+__device__ void attention_values_body(const ValuesArgs &a, int block) {
+  long bh = block;
+  if (bh >= long(a.B) * a.A) return;
+  attention_values_row(a, bh, a.probs + bh * a.T);
+}
 CKL_ENTRY_ATTR(attention_values, ValuesArgs, attention_values_body, kValuesBlock, )
+
+// softmax -> attention_values as one launch of attention_values's geometry (one workgroup per
+// (b, h), blockDim >= rowThreads, checked by the executor): lanes [0, rowThreads) compute the
+// row's softmax exactly as the softmax kernel does, writing probs and an LDS copy of the row
+// (T <= kChainSoftmaxRow floats of dynamic shared memory), then the workgroup reduces the values
+// from the LDS copy.
+__device__ void softmax__attention_values_body(const SoftmaxValuesChainArgs &a, int block) {
+  extern __shared__ float rowProbs[];
+  long bh = block;
+  if (bh >= long(a.values.B) * a.values.A) return;
+  const int rowThreads = a.softmax.rowThreads;
+  softmax_row(a.softmax, bh, int(threadIdx.x) % rowThreads, int(threadIdx.x) < rowThreads, rowProbs);
+  __syncthreads();
+  attention_values_row(a.values, bh, rowProbs);
+}
+CKL_ENTRY_ATTR(softmax__attention_values, SoftmaxValuesChainArgs, softmax__attention_values_body, kValuesBlock, )
 
 // ------------------------------------------------------------------ pointwise
 // add: dst = x + y; multiply: dst = x * y; silu: dst = v / (1 + exp(-v)) (workloads.py:145-167).
-struct CKL_ALIGN BinaryArgs { const float *x; const float *y; float *dst; int n; };
-struct CKL_ALIGN UnaryArgs { const float *src; float *dst; int n; };
 
 template <int Op> __device__ __forceinline__ float binary(float x, float y) { return Op == 0 ? x + y : x * y; }
 
@@ -738,6 +877,27 @@ __device__ void silu_body(const UnaryArgs &a, int block) {
 }
 CKL_ENTRY(silu, UnaryArgs, silu_body)
 
+// silu -> multiply as one launch of silu's geometry: element i (or float4 i) is activated,
+// written to silu's dst and multiplied by multiply's y in the same thread.
+__device__ void silu__multiply_body(const SiluMultiplyChainArgs &a, int block) {
+  long i = long(block) * kBlock + threadIdx.x;
+  const int n = a.silu.n;
+  if ((n & 3) == 0) {
+    if (i >= n / 4) return;
+    float4 v = reinterpret_cast<const float4 *>(a.silu.src)[i];
+    float4 act = make_float4(silu(v.x), silu(v.y), silu(v.z), silu(v.w));
+    if (a.silu.dst) reinterpret_cast<float4 *>(a.silu.dst)[i] = act;   // null: only multiply reads it
+    float4 y = reinterpret_cast<const float4 *>(a.multiply.y)[i];
+    reinterpret_cast<float4 *>(a.multiply.dst)[i] =
+        make_float4(binary<1>(act.x, y.x), binary<1>(act.y, y.y), binary<1>(act.z, y.z), binary<1>(act.w, y.w));
+  } else if (i < n) {
+    float act = silu(a.silu.src[i]);
+    if (a.silu.dst) a.silu.dst[i] = act;
+    a.multiply.dst[i] = binary<1>(act, a.multiply.y[i]);
+  }
+}
+CKL_ENTRY(silu__multiply, SiluMultiplyChainArgs, silu__multiply_body)
+
 // ------------------------------------------------------------------ greedy
 // tokens[b] = history[p, b] = first index of the maximum logit (strict '>' scan from index 0,
 // workloads.py:170-183): NaN logits never win, a NaN logit 0 is never displaced, +0 and -0 tie.
@@ -747,10 +907,6 @@ CKL_ENTRY(silu, UnaryArgs, silu_body)
 // the maximum key is the largest value at the smallest index) with an agent-scope atomic max
 // and bumps the row's counter; the last workgroup writes the token and resets key and counter.
 // workspace: uint64 key[B], then uint32 counter[B].
-struct CKL_ALIGN GreedyArgs {
-  const float *logits; int *tokens; int *history; const int *position; int B, V, T, chunks;
-  unsigned char *workspace;
-};
 constexpr int kGreedyChunk = 4096;
 
 __device__ __forceinline__ unsigned long long greedy_key(float v, int index) {
@@ -809,7 +965,6 @@ CKL_ENTRY(greedy, GreedyArgs, greedy_body)
 
 // ------------------------------------------------------------------ advance
 // position[0] += 1   (workloads.py:186-188)
-struct CKL_ALIGN AdvanceArgs { int *position; };
 __device__ void advance_body(const AdvanceArgs &a, int block) {
   if (block == 0 && threadIdx.x == 0) a.position[0] = a.position[0] + 1;
 }
@@ -817,7 +972,6 @@ CKL_ENTRY(advance, AdvanceArgs, advance_body)
 
 // ------------------------------------------------------------------ vector update
 // dst[i] = src[i] + bias for i < N   (examples/vector_pipeline.py:11-16)
-struct CKL_ALIGN UpdateArgs { const float *src; float *dst; float bias; int n; };
 __device__ void update_body(const UpdateArgs &a, int block) {
   long i = long(block) * kBlock + threadIdx.x;
   if ((a.n & 3) == 0) {

@@ -1,0 +1,351 @@
+// Chains: dependent library dispatches executed as one launch in the inferred graph.
+//
+// On MI355X every dependent kernel launch in a graph costs ~2.5 us of dispatch latency, which is
+// most of the time of the decode step's row-local kernels. The kernel library therefore has chain
+// entry points (csrc/kernels/library.hip) that run several dependent dispatches row by row in one
+// grid: rms_stats -> rms_apply, add -> rms_stats -> rms_apply, embedding -> rms_stats ->
+// rms_apply, silu -> multiply and softmax -> attention_values. The plan itself (nodes, edges,
+// argument blocks) is unchanged; only the inferred lowering contracts a chain into one unit.
+//
+// A chain is taken only when
+//   * each member depends directly on the previous one and the members' entry points and the
+//     chain entry point come from one code object;
+//   * the members' argument blocks agree (the buffer one member writes is the one the next
+//     reads, same shapes), read through the argument structs in csrc/kernels/args.h;
+//   * every buffer range a member writes is disjoint from every other range of the chain, or
+//     identical to it and accessed row by row in both (the chain runs member k of row r before
+//     member k-1 of row r' is done, which is only equivalent for such ranges);
+//   * contracting it (with the chains taken before) leaves the unit graph acyclic.
+// A hand-off buffer that only the chain reads (rms_stats's inv, softmax's probs, silu's output)
+// is kept in registers or LDS and not written when it is a temporary no other dispatch takes as
+// an argument: its range then cannot conflict with storage the planner reused for it.
+// Chains are found on one iteration of the plan and repeated for every iteration.
+#include "runtime.h"
+
+#include "../kernels/args.h"
+
+#include <algorithm>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <functional>
+#include <stdexcept>
+
+namespace ckl::rt {
+namespace {
+
+using namespace ckl::kernels;
+
+struct Range {
+  uint64_t begin = 0, end = 0;
+  bool written = false;
+  bool rowed = false;      // row r is touched only by the worker of row r
+  uint64_t rowBytes = 0;
+};
+
+Range rows(const void *p, uint64_t count, uint64_t rowBytes, bool written) {
+  uint64_t a = reinterpret_cast<uint64_t>(p);
+  return {a, a + count * rowBytes, written, true, rowBytes};
+}
+
+Range whole(const void *p, uint64_t bytes) {
+  uint64_t a = reinterpret_cast<uint64_t>(p);
+  return {a, a + bytes, false, false, 0};
+}
+
+bool tracing();
+
+bool hazardFree(const std::vector<Range> &ranges) {
+  for (size_t i = 0; i < ranges.size(); ++i)
+    for (size_t j = i + 1; j < ranges.size(); ++j) {
+      const Range &a = ranges[i], &b = ranges[j];
+      if (!a.written && !b.written) continue;
+      if (a.end <= b.begin || b.end <= a.begin) continue;
+      bool identical = a.begin == b.begin && a.end == b.end && a.rowed && b.rowed && a.rowBytes == b.rowBytes;
+      if (!identical) {
+        if (tracing())
+          std::fprintf(stderr, "[ckl chains] ranges %zu [%#llx, %#llx) and %zu [%#llx, %#llx) overlap\n", i,
+                       (unsigned long long)a.begin, (unsigned long long)a.end, j, (unsigned long long)b.begin,
+                       (unsigned long long)b.end);
+        return false;
+      }
+    }
+  return true;
+}
+
+template <typename T> T block(const Launch &launch) {
+  // Packed blocks are padded to 8 bytes, as are the aligned(8) structs.
+  if (launch.arguments.size() != sizeof(T))
+    throw std::logic_error("argument block of " + launch.name + " does not match the kernel library's layout");
+  T value;
+  std::memcpy(&value, launch.arguments.data(), sizeof(T));
+  return value;
+}
+
+constexpr const char *kOverlap = "buffers overlap in a way row-by-row execution would change";
+
+unsigned cdiv(uint64_t a, uint64_t b) { return unsigned((a + b - 1) / b); }
+
+// Geometry of the rms chains: one wave per row, four rows per 256-thread workgroup.
+void rowGeometry(Launch &out, int rowsCount) {
+  out.grid[0] = cdiv(uint64_t(rowsCount), 4);
+  out.block[0] = 256;
+  out.shared = 0;
+}
+
+template <typename T> void setArguments(Launch &out, const T &chain) {
+  out.arguments.resize(sizeof(T));
+  std::memcpy(out.arguments.data(), &chain, sizeof(T));
+}
+
+// A buffer that only the chain reads: a temporary (a plan resource placed in a heap) that no
+// dispatch outside the chain (in one iteration of the plan) takes as an argument. The chain keeps
+// such a hand-off in registers or LDS and does not write it (its pointer is cleared in the block).
+using Internal = std::function<bool(size_t member, const void *)>;
+using Members = std::vector<const Launch *>;
+
+const char *rmsTail(RmsStatsArgs &s, const RmsApplyArgs &p, size_t member, const Internal &internal,
+                    std::vector<Range> &ranges) {
+  if (s.x != p.x || s.inv != p.inv || s.B != p.B || s.C != p.C || s.B <= 0 || s.C <= 0 || p.layer < 0)
+    return "rms_stats and rms_apply disagree on x, inv or shape";
+  uint64_t row = 4ull * uint64_t(s.C);
+  if (internal(member, s.inv)) s.inv = nullptr;
+  ranges.push_back(rows(s.x, uint64_t(s.B), row, false));
+  if (s.inv) ranges.push_back(rows(s.inv, uint64_t(s.B), 4, true));
+  ranges.push_back(whole(p.gain + int64_t(p.layer) * s.C, row));
+  ranges.push_back(rows(p.dst, uint64_t(s.B), row, true));
+  return nullptr;
+}
+
+const char *rmsChain(const Members &m, const Internal &internal, Launch &out) {
+  RmsChainArgs c{block<RmsStatsArgs>(*m[0]), block<RmsApplyArgs>(*m[1])};
+  std::vector<Range> ranges;
+  if (const char *why = rmsTail(c.stats, c.apply, 0, internal, ranges)) return why;
+  if (!hazardFree(ranges)) return kOverlap;
+  rowGeometry(out, c.stats.B);
+  setArguments(out, c);
+  return nullptr;
+}
+
+const char *addRmsChain(const Members &m, const Internal &internal, Launch &out) {
+  AddRmsChainArgs c{block<BinaryArgs>(*m[0]), block<RmsStatsArgs>(*m[1]), block<RmsApplyArgs>(*m[2])};
+  std::vector<Range> ranges;
+  if (const char *why = rmsTail(c.stats, c.apply, 1, internal, ranges)) return why;
+  if (c.add.dst != c.stats.x || int64_t(c.add.n) != int64_t(c.stats.B) * c.stats.C)
+    return "add does not produce rms_stats's rows";
+  uint64_t row = 4ull * uint64_t(c.stats.C), count = uint64_t(c.stats.B);
+  ranges.push_back(rows(c.add.x, count, row, false));
+  ranges.push_back(rows(c.add.y, count, row, false));
+  ranges.push_back(rows(c.add.dst, count, row, true));
+  if (!hazardFree(ranges)) return kOverlap;
+  rowGeometry(out, c.stats.B);
+  setArguments(out, c);
+  return nullptr;
+}
+
+const char *embeddingRmsChain(const Members &m, const Internal &internal, Launch &out) {
+  EmbeddingRmsChainArgs c{block<EmbeddingArgs>(*m[0]), block<RmsStatsArgs>(*m[1]), block<RmsApplyArgs>(*m[2])};
+  const EmbeddingArgs &e = c.embedding;
+  std::vector<Range> ranges;
+  if (const char *why = rmsTail(c.stats, c.apply, 1, internal, ranges)) return why;
+  if (e.dst != c.stats.x || e.B != c.stats.B || e.C != c.stats.C || e.V <= 0)
+    return "embedding does not produce rms_stats's rows";
+  uint64_t row = 4ull * uint64_t(e.C), count = uint64_t(e.B);
+  ranges.push_back(rows(e.tokens, count, 4, false));
+  ranges.push_back(whole(e.table, uint64_t(e.V) * row));
+  ranges.push_back(rows(e.dst, count, row, true));
+  if (!hazardFree(ranges)) return kOverlap;
+  rowGeometry(out, e.B);
+  setArguments(out, c);
+  return nullptr;
+}
+
+const char *siluMultiplyChain(const Members &m, const Internal &internal, Launch &out) {
+  SiluMultiplyChainArgs c{block<UnaryArgs>(*m[0]), block<BinaryArgs>(*m[1])};
+  if (c.silu.dst != c.multiply.x || c.silu.n != c.multiply.n || c.silu.n <= 0)
+    return "multiply does not consume silu's output";
+  // Element i is owned by one thread in both members (float4 i when n % 4 == 0).
+  uint64_t n = uint64_t(c.silu.n);
+  if (internal(0, c.silu.dst)) c.silu.dst = nullptr;
+  std::vector<Range> ranges{rows(c.silu.src, n, 4, false), rows(c.multiply.y, n, 4, false), rows(c.multiply.dst, n, 4, true)};
+  if (c.silu.dst) ranges.push_back(rows(c.silu.dst, n, 4, true));
+  if (!hazardFree(ranges)) return kOverlap;
+  out.grid[0] = cdiv(n % 4 == 0 ? n / 4 : n, 256);
+  out.block[0] = 256;
+  out.shared = 0;
+  setArguments(out, c);
+  return nullptr;
+}
+
+const char *softmaxValuesChain(const Members &m, const Internal &internal, Launch &out) {
+  SoftmaxValuesChainArgs c{block<SoftmaxArgs>(*m[0]), block<ValuesArgs>(*m[1])};
+  const SoftmaxArgs &x = c.softmax;
+  const ValuesArgs &v = c.values;
+  const Launch &values = *m[1];
+  if (x.probs != v.probs || x.position != v.position || x.B != v.B || x.A != v.A || x.T != v.T)
+    return "attention_values does not consume softmax's rows";
+  if (x.B <= 0 || x.A <= 0 || x.T <= 0 || x.T > kChainSoftmaxRow || v.D <= 0 || v.layer < 0)
+    return "softmax row does not fit the chain's LDS copy";
+  if ((x.rowThreads != 64 && x.rowThreads != 256) || values.block[0] < unsigned(x.rowThreads))
+    return "attention_values workgroup is narrower than a softmax row";
+  if (values.grid[0] != unsigned(x.B) * unsigned(x.A)) return "attention_values grid is not one workgroup per row";
+  uint64_t bh = uint64_t(x.B) * uint64_t(x.A), row = 4ull * uint64_t(x.T);
+  uint64_t slab = bh * uint64_t(x.T) * uint64_t(v.D);
+  if (internal(0, x.probs)) c.softmax.probs = nullptr;
+  std::vector<Range> ranges{rows(x.scores, bh, row, false), whole(x.position, 4),
+                            whole(v.vc + int64_t(v.layer) * int64_t(slab), 4 * slab),
+                            rows(v.dst, bh, 4ull * uint64_t(v.D), true)};
+  if (c.softmax.probs) ranges.push_back(rows(x.probs, bh, row, true));
+  if (!hazardFree(ranges)) return kOverlap;
+  out.grid[0] = values.grid[0];
+  out.block[0] = values.block[0];
+  out.shared = unsigned(row);
+  setArguments(out, c);
+  return nullptr;
+}
+
+struct Rule {
+  std::vector<std::string> members;   // entry points, in dependency order
+  const char *entry;                  // chain entry point
+  const char *(*build)(const Members &, const Internal &, Launch &);   // null, or why not
+};
+
+const std::vector<Rule> &rules() {
+  static const std::vector<Rule> table = {
+      {{"ckl_add", "ckl_rms_stats", "ckl_rms_apply"}, "ckl_add__rms_stats__rms_apply", addRmsChain},
+      {{"ckl_embedding", "ckl_rms_stats", "ckl_rms_apply"}, "ckl_embedding__rms_stats__rms_apply", embeddingRmsChain},
+      {{"ckl_rms_stats", "ckl_rms_apply"}, "ckl_rms_stats__rms_apply", rmsChain},
+      {{"ckl_silu", "ckl_multiply"}, "ckl_silu__multiply", siluMultiplyChain},
+      {{"ckl_softmax", "ckl_attention_values"}, "ckl_softmax__attention_values", softmaxValuesChain},
+  };
+  return table;
+}
+
+bool singleGrid(const Launch &l) { return l.grid[1] == 1 && l.grid[2] == 1 && l.block[1] == 1 && l.block[2] == 1; }
+
+// Kahn's algorithm over the units given by `unit` (node -> unit id).
+bool acyclic(const Plan &plan, const std::vector<size_t> &unit, size_t units) {
+  std::vector<std::vector<size_t>> succ(units);
+  std::vector<size_t> indegree(units, 0);
+  for (size_t k = 0; k < plan.nodes.size(); ++k)
+    for (size_t d : plan.nodes[k].dependencies)
+      if (unit[d] != unit[k]) { succ[unit[d]].push_back(unit[k]); ++indegree[unit[k]]; }
+  std::vector<size_t> ready;
+  for (size_t u = 0; u < units; ++u) if (!indegree[u]) ready.push_back(u);
+  size_t seen = 0;
+  while (!ready.empty()) {
+    size_t u = ready.back();
+    ready.pop_back();
+    ++seen;
+    for (size_t s : succ[u]) if (!--indegree[s]) ready.push_back(s);
+  }
+  return seen == units;
+}
+
+} // namespace
+
+// CKL_CHAIN_TRACE=1 reports every chain considered and why it was not taken (stderr).
+namespace {
+bool tracing() {
+  static const bool on = [] {
+    const char *v = std::getenv("CKL_CHAIN_TRACE");
+    return v && std::strcmp(v, "1") == 0;
+  }();
+  return on;
+}
+
+void trace(size_t head, const Rule &rule, const char *outcome) {
+  if (tracing()) std::fprintf(stderr, "[ckl chains] node %zu %s: %s\n", head, rule.entry, outcome);
+}
+
+} // namespace
+
+std::vector<Chain> findChains(const Plan &plan, const std::vector<bool> &temporary) {
+  const size_t n = plan.nodes.size();
+  std::vector<std::vector<size_t>> successors(n);
+  for (size_t k = 0; k < n; ++k) for (size_t d : plan.nodes[k].dependencies) successors[d].push_back(k);
+  std::vector<size_t> unit(n);
+  for (size_t k = 0; k < n; ++k) unit[k] = k;
+  std::vector<bool> taken(n, false);
+  std::vector<Chain> chains;
+  for (size_t head = 0; head < n; ++head) {
+    if (taken[head]) continue;
+    const Launch &first = plan.nodes[head].launch;
+    for (const Rule &rule : rules()) {
+      if (first.name != rule.members[0] || !first.module || !singleGrid(first)) continue;
+      std::vector<size_t> members{head};
+      for (size_t k = 1; k < rule.members.size(); ++k) {
+        size_t found = n;
+        for (size_t s : successors[members.back()]) {
+          const Launch &l = plan.nodes[s].launch;
+          if (!taken[s] && l.name == rule.members[k] && l.module == first.module && singleGrid(l) && s < found) found = s;
+        }
+        if (found == n) break;
+        members.push_back(found);
+      }
+      if (members.size() != rule.members.size()) {
+        trace(head, rule, ("no dependent " + rule.members[members.size()] + " follows").c_str());
+        continue;
+      }
+      hipFunction_t function = nullptr, group = nullptr;
+      if (hipModuleGetFunction(&function, first.module, rule.entry) != hipSuccess) {
+        (void)hipGetLastError();
+        trace(head, rule, "the code object has no such entry point");
+        continue;
+      }
+      std::string groupName = std::string(rule.entry) + "_group";
+      if (hipModuleGetFunction(&group, first.module, groupName.c_str()) != hipSuccess) {
+        (void)hipGetLastError();
+        group = nullptr;
+      }
+      // The plan resources (logical buffers, whatever storage they share) that member `index`
+      // addresses with pointer `p` (the arguments of one dispatch are live together, so they
+      // never share storage); internal when each is a temporary no other dispatch takes.
+      auto internal = [&](size_t index, const void *p) {
+        std::vector<int64_t> ids;
+        const Launch &l = plan.nodes[members.at(index)].launch;
+        for (size_t slot = 0; slot < l.slotOffsets.size() && slot < l.slotResources.size(); ++slot) {
+          uint64_t word = 0;
+          if (l.slotResources[slot] < 0 || l.slotOffsets[slot] + 8 > l.arguments.size()) continue;
+          std::memcpy(&word, l.arguments.data() + l.slotOffsets[slot], 8);
+          if (word == reinterpret_cast<uint64_t>(p)) ids.push_back(l.slotResources[slot]);
+        }
+        if (ids.empty()) return false;
+        for (int64_t id : ids)
+          if (size_t(id) >= temporary.size() || !temporary[size_t(id)]) return false;
+        for (size_t k = 0; k < n; ++k) {
+          if (std::find(members.begin(), members.end(), k) != members.end()) continue;
+          for (int64_t id : plan.nodes[k].launch.slotResources)
+            if (std::find(ids.begin(), ids.end(), id) != ids.end()) return false;
+        }
+        return true;
+      };
+      std::vector<const Launch *> launches;
+      for (size_t m : members) launches.push_back(&plan.nodes[m].launch);
+      Launch fused;
+      fused.name = rule.entry;
+      fused.module = first.module;
+      fused.function = function;
+      fused.groupFunction = group;
+      if (const char *why = rule.build(launches, internal, fused)) {
+        trace(head, rule, why);
+        continue;
+      }
+      std::vector<size_t> trial = unit;
+      for (size_t m : members) trial[m] = head;
+      // Unit ids stay node indices: count them as the node range.
+      if (!acyclic(plan, trial, n)) {
+        trace(head, rule, "contracting it would create a cycle");
+        continue;
+      }
+      trace(head, rule, "taken");
+      unit = std::move(trial);
+      for (size_t m : members) taken[m] = true;
+      chains.push_back({std::move(members), std::move(fused)});
+      break;
+    }
+  }
+  return chains;
+}
+
+} // namespace ckl::rt

@@ -157,15 +157,16 @@ void launchOrdinary(const Plan &plan, hipStream_t stream) {
   for (const PlanNode &node : plan.nodes) launchOne(node.launch, stream);
 }
 
-// A unit of the inferred graph: one dispatch, or sibling dispatches of one library family
-// executed by the family's group entry point (each member keeps its own grid range).
+// A unit of the inferred graph: one dispatch, a chain of dependent dispatches run by a chain
+// entry point, or sibling units of one family executed by the family's group entry point (each
+// member keeps its own grid range).
 struct Unit {
   std::vector<size_t> members;
   Launch launch;
 };
 
-Launch groupLaunch(const Plan &plan, const std::vector<size_t> &members) {
-  const Launch &first = plan.nodes[members[0]].launch;
+Launch groupLaunch(const std::vector<const Launch *> &members) {
+  const Launch &first = *members[0];
   Launch out = first;
   out.function = first.groupFunction;
   out.groupFunction = nullptr;
@@ -174,10 +175,9 @@ Launch groupLaunch(const Plan &plan, const std::vector<size_t> &members) {
   int32_t start = 0;
   std::vector<int32_t> starts;
   for (size_t k = 0; k < members.size(); ++k) {
-    const Launch &m = plan.nodes[members[k]].launch;
-    std::memcpy(blob.data() + k * stride, m.arguments.data(), stride);
+    std::memcpy(blob.data() + k * stride, members[k]->arguments.data(), stride);
     starts.push_back(start);
-    start += int32_t(m.grid[0]);
+    start += int32_t(members[k]->grid[0]);
   }
   starts.push_back(start);
   while (starts.size() < kMaxGroup + 1) starts.push_back(start);
@@ -190,43 +190,92 @@ Launch groupLaunch(const Plan &plan, const std::vector<size_t> &members) {
   return out;
 }
 
-std::vector<Unit> groupPlan(const Plan &plan) {
-  std::vector<size_t> level(plan.nodes.size(), 0);
-  size_t maxLevel = 0;
-  for (size_t k = 0; k < plan.nodes.size(); ++k) {
-    for (size_t d : plan.nodes[k].dependencies) level[k] = std::max(level[k], level[d] + 1);
-    maxLevel = std::max(maxLevel, level[k]);
+// The inferred lowering: library chains are contracted into single units, units are levelled by
+// their longest dependency path, and same-level units of one family become one group launch.
+// `chains` were found on one iteration of `iterations` (the plan's nodes repeat with that period).
+std::vector<Unit> groupPlan(const Plan &plan, const std::vector<Chain> &found, size_t iterations) {
+  const size_t n = plan.nodes.size();
+  const size_t period = n / iterations;
+  std::vector<Chain> chains;
+  for (size_t it = 0; it < iterations; ++it)
+    for (const Chain &c : found) {
+      Chain copy = c;
+      for (size_t &m : copy.members) m += it * period;
+      chains.push_back(std::move(copy));
+    }
+  std::vector<int> chainAt(n, -1);
+  for (size_t c = 0; c < chains.size(); ++c) for (size_t m : chains[c].members) chainAt[m] = int(c);
+  std::vector<size_t> unitOf(n);
+  std::vector<Unit> base;
+  for (size_t k = 0; k < n; ++k) {
+    if (chainAt[k] >= 0) {
+      const Chain &c = chains[size_t(chainAt[k])];
+      if (c.members[0] != k) { unitOf[k] = unitOf[c.members[0]]; continue; }   // members ascend
+      unitOf[k] = base.size();
+      base.push_back({c.members, c.launch});
+    } else {
+      unitOf[k] = base.size();
+      base.push_back({{k}, plan.nodes[k].launch});
+    }
   }
+  const size_t units = base.size();
+  std::vector<std::vector<size_t>> succ(units);
+  std::vector<size_t> indegree(units, 0), level(units, 0);
+  for (size_t k = 0; k < n; ++k)
+    for (size_t d : plan.nodes[k].dependencies)
+      if (unitOf[d] != unitOf[k]) { succ[unitOf[d]].push_back(unitOf[k]); ++indegree[unitOf[k]]; }
+  std::vector<size_t> ready, order;
+  for (size_t u = 0; u < units; ++u) if (!indegree[u]) ready.push_back(u);
+  while (!ready.empty()) {
+    size_t u = ready.back();
+    ready.pop_back();
+    order.push_back(u);
+    for (size_t s : succ[u]) {
+      level[s] = std::max(level[s], level[u] + 1);
+      if (!--indegree[s]) ready.push_back(s);
+    }
+  }
+  if (order.size() != units) throw std::logic_error("contracted inferred graph has a cycle");
+  size_t maxLevel = 0;
+  for (size_t u = 0; u < units; ++u) maxLevel = std::max(maxLevel, level[u]);
   std::vector<std::vector<size_t>> byLevel(maxLevel + 1);
-  for (size_t k = 0; k < plan.nodes.size(); ++k) byLevel[level[k]].push_back(k);
-  std::vector<Unit> units;
-  for (const auto &nodes : byLevel) {
+  for (size_t u = 0; u < units; ++u) byLevel[level[u]].push_back(u);
+  std::vector<Unit> out;
+  for (const auto &members : byLevel) {
     std::vector<std::vector<size_t>> buckets;
-    for (size_t k : nodes) {
-      const Launch &l = plan.nodes[k].launch;
+    for (size_t u : members) {
+      const Launch &l = base[u].launch;
       bool groupable = l.groupFunction && l.grid[1] == 1 && l.grid[2] == 1;
       bool placed = false;
       if (groupable)
         for (auto &bucket : buckets) {
-          const Launch &b = plan.nodes[bucket[0]].launch;
+          const Launch &b = base[bucket[0]].launch;
           if (bucket.size() < kMaxGroup && b.function == l.function && b.groupFunction &&
               std::equal(b.block, b.block + 3, l.block) && b.shared == l.shared &&
               b.arguments.size() == l.arguments.size() && b.grid[1] == 1 && b.grid[2] == 1) {
-            bucket.push_back(k);
+            bucket.push_back(u);
             placed = true;
             break;
           }
         }
-      if (!placed) buckets.push_back({k});
+      if (!placed) buckets.push_back({u});
     }
     for (auto &bucket : buckets) {
-      Unit u;
-      u.members = bucket;
-      u.launch = bucket.size() == 1 ? plan.nodes[bucket[0]].launch : groupLaunch(plan, bucket);
-      units.push_back(std::move(u));
+      if (bucket.size() == 1) {
+        out.push_back(std::move(base[bucket[0]]));
+        continue;
+      }
+      Unit g;
+      std::vector<const Launch *> launches;
+      for (size_t u : bucket) {
+        g.members.insert(g.members.end(), base[u].members.begin(), base[u].members.end());
+        launches.push_back(&base[u].launch);
+      }
+      g.launch = groupLaunch(launches);
+      out.push_back(std::move(g));
     }
   }
-  return units;
+  return out;
 }
 
 std::unique_ptr<GraphExec> captureUnits(const std::vector<Launch> &launches, hipStream_t stream) {
@@ -322,8 +371,8 @@ GraphExec &Invocation::graphFor(int mode, uint64_t batch) {
       for (size_t k = 0; k < repeated.nodes.size(); ++k) units.push_back({{k}, repeated.nodes[k].launch});
       slot = explicitGraph(repeated, units);
     } else {
-      // Sibling groups ordered by DAG level, captured as one chain of launches.
-      std::vector<Unit> units = groupPlan(repeated);
+      // Chains contracted, sibling groups ordered by DAG level, captured as one launch chain.
+      std::vector<Unit> units = groupPlan(repeated, findChains(plan, temporaryResources), batch);
       std::vector<Launch> launches;
       for (const Unit &u : units) launches.push_back(u.launch);
       slot = captureUnits(launches, stream);
@@ -430,13 +479,14 @@ template <typename F> static void callback(void *opaque, F action) {
   }
 }
 
-static void appendArgument(Launch &launch, const void *data, uint64_t size) {
+static void appendArgument(Launch &launch, const void *data, uint64_t size, int64_t resource = -1) {
   if (!data || !size) throw std::invalid_argument("physical kernel argument must not be empty");
   size_t align = (size == 1 || size == 2 || size == 4 || size == 8) ? size : 1;
   size_t offset = (launch.arguments.size() + align - 1) & ~(align - 1);
   launch.arguments.resize(offset + size, 0);
   std::memcpy(launch.arguments.data() + offset, data, size);
   launch.slotOffsets.push_back(offset);
+  launch.slotResources.push_back(resource);
 }
 
 std::shared_ptr<Invocation> bind(const std::shared_ptr<ProgramState> &programIn, std::shared_ptr<Device> device,
@@ -515,6 +565,8 @@ extern "C" void ckl_heap(void *frame, uint64_t id, uint64_t bytes) {
 extern "C" void ckl_resource(void *frame, uint64_t id, uint64_t heap, uint64_t offset, void *external) {
   ckl::rt::callback(frame, [&](Invocation &f) {
     if (f.resources.size() <= id) f.resources.resize(id + 1);
+    if (f.temporaryResources.size() <= id) f.temporaryResources.resize(id + 1, false);
+    f.temporaryResources[id] = !external;
     if (external) f.resources[id] = *static_cast<uint64_t *>(external);
     else {
       const auto &h = f.heaps.at(heap);
@@ -530,6 +582,7 @@ extern "C" void ckl_kernel(void *frame, const char *name, uint64_t gx, uint64_t 
     if (!f.module) throw std::invalid_argument("ckl_kernel requires a loaded module (ckl_begin)");
     Launch launch;
     launch.name = name;
+    launch.module = f.module;
     ckl::rt::check(hipModuleGetFunction(&launch.function, f.module, name), "hipModuleGetFunction");
     hipFunction_t group = nullptr;
     std::string groupName = std::string(name) + "_group";
@@ -549,7 +602,7 @@ extern "C" void ckl_kernel(void *frame, const char *name, uint64_t gx, uint64_t 
 extern "C" void ckl_argument_resource(void *frame, uint64_t id, uint64_t offset) {
   ckl::rt::callback(frame, [&](Invocation &f) {
     uint64_t address = f.resources.at(id) + offset;
-    ckl::rt::appendArgument(f.pending, &address, sizeof address);
+    ckl::rt::appendArgument(f.pending, &address, sizeof address, int64_t(id));
   });
 }
 

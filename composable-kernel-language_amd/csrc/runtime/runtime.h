@@ -54,6 +54,7 @@ std::shared_ptr<Buffer> sliceBuffer(const std::shared_ptr<Buffer> &buffer, uint6
 
 // One resolved kernel launch: function, geometry and the packed argument struct.
 struct Launch {
+  hipModule_t module = nullptr;             // code object the function comes from
   hipFunction_t function = nullptr;
   hipFunction_t groupFunction = nullptr;   // sibling-group entry point, when the artifact has one
   std::string name;
@@ -62,6 +63,7 @@ struct Launch {
   unsigned shared = 0;
   std::vector<uint8_t> arguments;           // kernarg bytes (natural alignment, padded to 8)
   std::vector<size_t> slotOffsets;
+  std::vector<int64_t> slotResources;       // per slot: the plan resource it addresses, or -1
 };
 
 struct PlanNode {
@@ -74,6 +76,16 @@ struct Plan {
   size_t addKernel(Launch launch, std::vector<size_t> dependencies);
   Plan repeat(size_t iterations) const;      // roots of iteration i+1 follow every leaf of i
 };
+
+// Dependent dispatches the inferred graph runs as one launch of a kernel-library chain entry
+// point (csrc/runtime/chains.cpp): `members` in dependency order, `launch` with the members'
+// argument blocks back to back. Found on one iteration of the plan; `temporary[id]` tells
+// whether plan resource `id` is a heap temporary (a buffer no caller can observe).
+struct Chain {
+  std::vector<size_t> members;
+  Launch launch;
+};
+std::vector<Chain> findChains(const Plan &plan, const std::vector<bool> &temporary);
 
 struct GraphExec {
   hipGraph_t graph = nullptr;
@@ -94,6 +106,7 @@ struct Invocation {
   std::vector<std::shared_ptr<Buffer>> buffers;     // keeps bound buffers alive
   std::vector<std::shared_ptr<Buffer>> workspaces;  // private library-kernel workspaces (zeroed at bind)
   std::vector<uint64_t> resources;
+  std::vector<bool> temporaryResources;             // resource id -> placed in a heap
   Plan plan;
   hipModule_t module = nullptr;                     // current module during plan construction
   Launch pending;
@@ -142,8 +155,9 @@ struct Argument {
 std::shared_ptr<Invocation> bind(const std::shared_ptr<ProgramState> &program, std::shared_ptr<Device> device,
                                  const std::vector<Argument> &arguments);
 
-// Graph policy for mode 1: group sibling dispatches of one library family into one launch and
-// chain the result (default), or keep one graph node per dispatch with real branches.
+// Graph policy for mode 1: contract library chains, group sibling dispatches of one library
+// family into one launch and capture the result as one launch chain (default), or keep one graph
+// node per dispatch with real branches.
 enum class BranchPolicy { Grouped, Branches };
 BranchPolicy branchPolicy();
 

@@ -282,7 +282,8 @@ def linear_tiling(b: int, i: int, o: int) -> dict:
         split = _cdiv(i, chunk)
         rows, row_tiles = _cdiv(b, 32) * 32, _cdiv(b, 32)
         shared = 3 * j * 16 * 64 * 4
-        entry = f"ckl_linear_mfma{j}"
+        stage = 1
+        entry = f"ckl_linear_mfma{j}x{stage}"
         block = BLOCK
     elif b <= LINEAR_VECTOR_ROWS:
         tiles = _cdiv(o, 64)

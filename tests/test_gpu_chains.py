@@ -1,0 +1,97 @@
+"""Library chains in the inferred graph (csrc/runtime/chains.cpp): contracted launches leave exactly
+the state the ordinary launches leave, bit for bit, the decode step runs in 11 launches per layer
+plus 4, and a chain whose buffers overlap in a way row-by-row execution would change runs unfused."""
+import numpy as np
+import pytest
+
+import ckl
+from oracle import decoder as oracle
+from programs.decoder import rms_apply, rms_stats
+from programs.decoder_config import CONFIGS, Config
+from programs.harness import MUTABLE, DecoderSession
+
+pytestmark = pytest.mark.gpu
+
+REFERENCE_SMALL = Config(batch=1, hidden=64, heads=4, layers=2, ffn=128, vocab=256, context=8, steps=16)
+AWKWARD = Config(batch=3, hidden=48, heads=3, layers=1, ffn=80, vocab=129, context=3, steps=16)
+# Rows not a multiple of 4 floats (scalar paths of the rms and silu chains), D = 14.
+ODD = Config(batch=2, hidden=42, heads=3, layers=2, ffn=31, vocab=70, context=5, steps=6)
+
+
+def chained_launches(layers):
+    # embedding+rms; per layer: QKV, rope pair, append, scores, softmax+values, O, add+rms,
+    # gate/up, silu+multiply, down, add+rms; then lm head, greedy, advance.
+    return 1 + 11 * layers + 3
+
+
+@pytest.mark.parametrize("config", [CONFIGS["small"], REFERENCE_SMALL, AWKWARD, ODD],
+                         ids=["small", "reference_small", "awkward", "odd"])
+def test_chained_graph_is_bit_identical_to_ordinary(device, config):
+    c = config
+    initial, _ = oracle.make_inputs(c, 7, init="reference")
+    session = DecoderSession(c, device, arrays=initial)
+    reference = oracle.expected(initial, c, c.steps)
+    for reuse, inv in session.invocations.items():
+        launches = inv.launch_count(mode="graph", batch_size=1)
+        if reuse:
+            # Storage reuse may place attention's output over the scores it is computed from;
+            # that softmax -> attention_values chain then runs as two launches.
+            assert chained_launches(c.layers) <= launches <= chained_launches(c.layers) + c.layers
+        else:
+            assert launches == chained_launches(c.layers)
+        assert inv.launch_count(mode="graph", batch_size=c.steps) == c.steps * launches
+        results = {}
+        for mode, group in (("ordinary", 1), ("graph", 1), ("graph", c.steps)):
+            session.state.reset()
+            for _ in range(c.steps // group):
+                inv.run(mode=mode, batch_size=group)
+            session.state.verify(reference)
+            results[(mode, group)] = {name: session.state.download(name) for name in MUTABLE}
+        for key in (("graph", 1), ("graph", c.steps)):
+            for name in MUTABLE:
+                assert np.array_equal(results[key][name], results[("ordinary", 1)][name]), (reuse, key, name)
+
+
+_B, _C = ckl.dim("B"), ckl.dim("C")
+
+
+@ckl.program
+def normalize(x: ckl.Buffer[ckl.f32, (_B, _C)], inv: ckl.Buffer[ckl.f32, (_B,)],
+              gain: ckl.Buffer[ckl.f32, (1, _C)], dst: ckl.Buffer[ckl.f32, (_B, _C)], eps: ckl.f32) -> None:
+    ckl.launch(rms_stats, x, inv, eps, grid=(ckl.cdiv(_B, 32),), block=(32,))
+    ckl.launch(rms_apply, x, inv, gain, dst, 0, grid=(ckl.cdiv(_C, 64), _B), block=(64,))
+
+
+@pytest.mark.parametrize("overlap", [False, True], ids=["disjoint", "inv_aliases_gain"])
+def test_rms_chain_respects_overlapping_buffers(device, overlap):
+    b, c = 4, 64
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((b, c)).astype(np.float32)
+    gain = rng.standard_normal((1, c)).astype(np.float32)
+    sig = {"x": ckl.BufferSpec((b, c), ckl.f32), "inv": ckl.BufferSpec((b,), ckl.f32),
+           "gain": ckl.BufferSpec((1, c), ckl.f32), "dst": ckl.BufferSpec((b, c), ckl.f32), "eps": ckl.f32}
+    compiled = normalize.lower(signature=sig).compile(fuse_pointwise=False)
+    assert '"ckl_rms_stats"' in compiled.executable_ir and '"ckl_rms_apply"' in compiled.executable_ir
+    bx = device.empty(sig["x"])
+    bg = device.empty(sig["gain"])
+    bd = device.empty(sig["dst"])
+    # With overlap, inv is the first B floats of gain: rms_apply must see the gains rms_stats
+    # overwrote, which running row by row would not guarantee.
+    bi = device.import_buffer(bg.address, sig["inv"], owner=bg) if overlap else device.empty(sig["inv"])
+    inv = compiled.bind(bx, bi, bg, bd, 1e-5)
+    assert inv.launch_count(mode="graph", batch_size=1) == (2 if overlap else 1)
+    outputs = {}
+    for mode in ("ordinary", "graph"):
+        bx.copy_from_host(x)
+        bg.copy_from_host(gain)
+        inv.run(mode=mode)
+        got = np.empty((b, c), np.float32)
+        bd.copy_to_host(got)
+        outputs[mode] = got
+    assert np.array_equal(outputs["ordinary"], outputs["graph"])
+    inverse = 1.0 / np.sqrt((x.astype(np.float64) ** 2).mean(axis=1) + 1e-5)
+    g = gain[0].astype(np.float64).copy()
+    if overlap:
+        g[:b] = inverse.astype(np.float32)
+    expected = x * inverse[:, None] * g[None, :]
+    assert np.allclose(outputs["ordinary"], expected, rtol=1e-5, atol=1e-6)
