@@ -7,10 +7,10 @@
 // the block to 8 bytes, which is the layout of these aligned(8) structs.
 //
 // Chain entry points (several dependent dispatches executed as one launch in the inferred graph)
-// take the member blocks back to back: struct { First first; Second second; ... }. Each member
-// is aligned(8) with a size that is a multiple of 8, so the executor concatenates the members'
-// packed blocks unchanged. The executor reads these structs (csrc/runtime/chains.cpp) to decide
-// whether a chain may run fused; the kernels read them to run it.
+// take the member blocks back to back: struct { First first; Second second; ... }. The executor
+// (csrc/runtime/chains.cpp) reads the members' packed blocks through these structs to decide
+// whether a chain may run fused, and fills the chain block from them, clearing the pointers of
+// hand-off buffers that only the chain reads (the kernels then do not write them).
 #pragma once
 
 #include <stdint.h>
@@ -70,8 +70,10 @@ struct CKL_ALIGN AddRmsChainArgs { BinaryArgs add; RmsStatsArgs stats; RmsApplyA
 struct CKL_ALIGN EmbeddingRmsChainArgs { EmbeddingArgs embedding; RmsStatsArgs stats; RmsApplyArgs apply; };
 struct CKL_ALIGN SiluMultiplyChainArgs { UnaryArgs silu; BinaryArgs multiply; };
 struct CKL_ALIGN SoftmaxValuesChainArgs { SoftmaxArgs softmax; ValuesArgs values; };
+struct CKL_ALIGN AttentionChainArgs { ScoresArgs scores; SoftmaxArgs softmax; ValuesArgs values; };
+struct CKL_ALIGN RopeAppendChainArgs { RopeArgs q; RopeArgs k; AppendArgs append; };
 
-// Largest row (in floats) a softmax -> attention_values chain keeps in LDS.
+// Largest row (in floats) an attention chain keeps in LDS.
 constexpr int kChainSoftmaxRow = 8192;
 
 } // namespace ckl::kernels

@@ -585,6 +585,10 @@ CKL_ENTRY_ATTR(linear_mfma4x2, LinearArgs, (linear_mfma_body<4, 2>), kBlock, CKL
 // ------------------------------------------------------------------ rope
 // Adjacent-pair rotation at position p (workloads.py:72-85):
 //   dst[b,c] = s[b,c]*cos - s[b,c+1]*sin; dst[b,c+1] = s[b,c]*sin + s[b,c+1]*cos, c = h*2R + 2r.
+// (first*cos - second*sin, first*sin + second*cos) with explicit FMAs, shared by rope and its chain.
+__device__ __forceinline__ float2 rotate(float2 s, float2 cs) {
+  return make_float2(__builtin_fmaf(s.x, cs.x, -(s.y * cs.y)), __builtin_fmaf(s.x, cs.y, s.y * cs.x));
+}
 __device__ void rope_body(const RopeArgs &a, int block) {
   long i = long(block) * kBlock + threadIdx.x;
   long pairs = long(a.B) * a.A * a.R;
@@ -597,7 +601,7 @@ __device__ void rope_body(const RopeArgs &a, int block) {
   long c = long(b) * (2L * a.R * a.A) + long(h) * (2 * a.R) + 2 * r;
   float2 s = *reinterpret_cast<const float2 *>(a.src + c);
   float2 cs = *reinterpret_cast<const float2 *>(a.table + (long(p) * a.R + r) * 2);
-  *reinterpret_cast<float2 *>(a.dst + c) = make_float2(s.x * cs.x - s.y * cs.y, s.x * cs.y + s.y * cs.x);
+  *reinterpret_cast<float2 *>(a.dst + c) = rotate(s, cs);
 }
 CKL_ENTRY(rope, RopeArgs, rope_body)
 
@@ -627,6 +631,32 @@ __device__ void append_kv_body(const AppendArgs &a, int block) {
 }
 CKL_ENTRY(append_kv, AppendArgs, append_kv_body)
 
+// rope(q), rope(k) -> append_kv as one launch of rope's geometry: thread (b, h, r) rotates the
+// pair (2r, 2r+1) of q and of k, writes q's (and k's, unless only append reads it), and appends
+// the rotated k pair and v's pair to the caches at the current position. (D = 2R, so element
+// h*D + 2r of k and v is the same index c as the rotated pair.)
+__device__ void rope__rope__append_kv_body(const RopeAppendChainArgs &a, int block) {
+  const RopeArgs &q = a.q, &k = a.k;
+  const AppendArgs &ap = a.append;
+  long i = long(block) * kBlock + threadIdx.x;
+  long pairs = long(q.B) * q.A * q.R;
+  if (i >= pairs) return;
+  int p = load_position(q.position);
+  if (p < 0 || p >= q.T) return;
+  int r = int(i % q.R);
+  long bh = i / q.R;
+  int h = int(bh % q.A), b = int(bh / q.A);
+  long c = long(b) * (2L * q.R * q.A) + long(h) * (2 * q.R) + 2 * r;
+  float2 cs = *reinterpret_cast<const float2 *>(q.table + (long(p) * q.R + r) * 2);
+  *reinterpret_cast<float2 *>(q.dst + c) = rotate(*reinterpret_cast<const float2 *>(q.src + c), cs);
+  float2 kr = rotate(*reinterpret_cast<const float2 *>(k.src + c), cs);
+  if (k.dst) *reinterpret_cast<float2 *>(k.dst + c) = kr;
+  long row = (((long(ap.layer) * ap.B * ap.A) + bh) * ap.T + p) * ap.D + 2 * r;
+  *reinterpret_cast<float2 *>(ap.kc + row) = kr;
+  *reinterpret_cast<float2 *>(ap.vc + row) = *reinterpret_cast<const float2 *>(ap.v + c);
+}
+CKL_ENTRY(rope__rope__append_kv, RopeAppendChainArgs, rope__rope__append_kv_body)
+
 // ------------------------------------------------------------------ attention_scores
 // scores[b,h,t] = (sum_d q[b,h*D+d] * kc[layer,b,h,t,d]) * scale for t <= p (workloads.py:100-111).
 // One 256-thread workgroup per (b, h, 256-row chunk); each wave owns 64 consecutive cache rows.
@@ -634,6 +664,18 @@ CKL_ENTRY(append_kv, AppendArgs, append_kv_body)
 // reducing any of them, so ~kScoreBatch KB per wave are in flight. Row addresses past the end
 // re-read an early row of the wave and their results are dropped (the loads stay unpredicated).
 constexpr int kScoreBatch = 8;
+// Row arithmetic shared by attention_scores and its chain: a lane's 4-element partial dot
+// product (explicit FMAs), summed over the row's D/4 lanes by group_sum; rows the vector layout
+// does not cover use the sequential dot product.
+__device__ __forceinline__ float dot4(float4 q, float4 k) {
+  return __builtin_fmaf(q.w, k.w, __builtin_fmaf(q.z, k.z, __builtin_fmaf(q.y, k.y, q.x * k.x)));
+}
+__device__ __forceinline__ float score_scalar(const float *q, const float *key, int D) {
+  float v = 0.f;
+  for (int d = 0; d < D; ++d) v = __builtin_fmaf(q[d], key[d], v);
+  return v;
+}
+__device__ __forceinline__ bool scores_vector_layout(int D) { return (D & 3) == 0 && D <= 256 && (64 % (D / 4)) == 0; }
 __device__ void attention_scores_body(const ScoresArgs &a, int block) {
   int chunks = (a.T + kBlock - 1) / kBlock;
   int chunk = block % chunks;
@@ -647,7 +689,7 @@ __device__ void attention_scores_body(const ScoresArgs &a, int block) {
   const float *keys = a.kc + (long(a.layer) * a.B * a.A + bh) * long(a.T) * a.D;
   float *scores = a.scores + bh * a.T;
   int tEnd = min(t0 + kBlock, end);
-  if ((a.D & 3) == 0 && a.D <= 256 && (64 % (a.D / 4)) == 0) {
+  if (scores_vector_layout(a.D)) {
     const int width = a.D / 4;                   // lanes per row
     const int rowsPerLoad = 64 / width;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -664,18 +706,13 @@ __device__ void attention_scores_body(const ScoresArgs &a, int block) {
       }
 #pragma unroll
       for (int u = 0; u < kScoreBatch; ++u) {
-        float v = qv.x * kv[u].x + qv.y * kv[u].y + qv.z * kv[u].z + qv.w * kv[u].w;
-        v = group_sum(v, width);
+        float v = group_sum(dot4(qv, kv[u]), width);
         int t = base + u * rowsPerLoad + sub;
         if (part == 0 && t < w1) scores[t] = v * a.scale;
       }
     }
   } else {
-    for (int t = t0 + threadIdx.x; t < tEnd; t += kBlock) {
-      float v = 0.f;
-      for (int d = 0; d < a.D; ++d) v += q[d] * keys[long(t) * a.D + d];
-      scores[t] = v * a.scale;
-    }
+    for (int t = t0 + threadIdx.x; t < tEnd; t += kBlock) scores[t] = score_scalar(q, keys + long(t) * a.D, a.D) * a.scale;
   }
 }
 CKL_ENTRY(attention_scores, ScoresArgs, attention_scores_body)
@@ -702,14 +739,15 @@ template <bool IsMax> __device__ __forceinline__ float row_reduce(float v, int r
   return r;
 }
 
-// Softmax of row `row` by the lanes with local index `local` < rowThreads (inactive lanes only
-// take part in the synchronization). Probabilities go to a.probs and, when `stage` is given, to
-// stage[t] as well.
-__device__ __forceinline__ void softmax_row(const SoftmaxArgs &a, long row, int local, bool active, float *stage) {
+// Softmax of row `row` (scores `s`: a.scores' row, or its LDS copy in a chain) by the lanes with
+// local index `local` < rowThreads (inactive lanes only take part in the synchronization).
+// Probabilities go to a.probs (unless null) and, when `stage` is given, to stage[t] as well;
+// `stage` may be `s` itself: every lane reads its elements before it writes them.
+__device__ __forceinline__ void softmax_row(const SoftmaxArgs &a, const float *s, long row, int local, bool active,
+                                            float *stage) {
   int p = load_position(a.position);
   int end = min(p + 1, a.T);
   if (p < 0) end = 0;
-  const float *s = a.scores + (active ? row : 0) * a.T;
   float *out = a.probs ? a.probs + (active ? row : 0) * a.T : nullptr;   // null in a chain: LDS only
   if (end <= a.rowThreads * kSoftmaxPerLane) {
     float v[kSoftmaxPerLane];
@@ -759,7 +797,7 @@ __device__ void softmax_body(const SoftmaxArgs &a, int block) {
   const int local = threadIdx.x % a.rowThreads;
   long row = long(block) * rowsPerBlock + threadIdx.x / a.rowThreads;
   const bool active = row < long(a.B) * a.A;       // uniform per row group (rowThreads divides kBlock)
-  softmax_row(a, row, local, active, nullptr);
+  softmax_row(a, a.scores + (active ? row : 0) * a.T, row, local, active, nullptr);
 }
 CKL_ENTRY(softmax, SoftmaxArgs, softmax_body)
 
@@ -837,11 +875,69 @@ __device__ void softmax__attention_values_body(const SoftmaxValuesChainArgs &a, 
   long bh = block;
   if (bh >= long(a.values.B) * a.values.A) return;
   const int rowThreads = a.softmax.rowThreads;
-  softmax_row(a.softmax, bh, int(threadIdx.x) % rowThreads, int(threadIdx.x) < rowThreads, rowProbs);
+  softmax_row(a.softmax, a.softmax.scores + bh * a.softmax.T, bh, int(threadIdx.x) % rowThreads,
+              int(threadIdx.x) < rowThreads, rowProbs);
   __syncthreads();
   attention_values_row(a.values, bh, rowProbs);
 }
 CKL_ENTRY_ATTR(softmax__attention_values, SoftmaxValuesChainArgs, softmax__attention_values_body, kValuesBlock, )
+
+// attention_scores -> softmax -> attention_values as one launch of attention_values's geometry
+// (one workgroup per (b, h)): the workgroup computes the row's scores into LDS (the waves stride
+// over cache rows, kScoreBatch row loads per lane in flight, each row reduced exactly as
+// attention_scores does), the softmax in place in LDS, then the values from LDS. Scores and
+// probabilities are also written to global memory unless the executor cleared those pointers
+// (only the chain reads them).
+__device__ void attention_scores__softmax__attention_values_body(const AttentionChainArgs &a, int block) {
+  extern __shared__ float rowScores[];
+  const ScoresArgs &sc = a.scores;
+  long bh = block;
+  if (bh >= long(a.values.B) * a.values.A) return;
+  int p = load_position(sc.position);
+  int end = min(p + 1, sc.T);
+  if (p < 0) end = 0;
+  const float *q = sc.q + bh * sc.D;
+  const float *keys = sc.kc + (long(sc.layer) * sc.B * sc.A + bh) * long(sc.T) * sc.D;
+  float *scores = sc.scores ? sc.scores + bh * sc.T : nullptr;
+  if (scores_vector_layout(sc.D)) {
+    const int width = sc.D / 4, rowsPerLoad = 64 / width;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
+    const int sub = lane / width, part = lane % width;
+    const float4 qv = reinterpret_cast<const float4 *>(q)[part];
+    const int step = waves * kScoreBatch * rowsPerLoad;
+    for (int base = wave * kScoreBatch * rowsPerLoad; base < end; base += step) {
+      float4 kv[kScoreBatch];
+#pragma unroll
+      for (int u = 0; u < kScoreBatch; ++u) {
+        int t = base + u * rowsPerLoad + sub;
+        t = t < end ? t : min(sub, end - 1);      // past the end: re-read an early row, dropped
+        kv[u] = reinterpret_cast<const float4 *>(keys + long(t) * sc.D)[part];
+      }
+#pragma unroll
+      for (int u = 0; u < kScoreBatch; ++u) {
+        float v = group_sum(dot4(qv, kv[u]), width) * sc.scale;
+        int t = base + u * rowsPerLoad + sub;
+        if (part == 0 && t < end) {
+          rowScores[t] = v;
+          if (scores) scores[t] = v;
+        }
+      }
+    }
+  } else {
+    for (int t = threadIdx.x; t < end; t += blockDim.x) {
+      float v = score_scalar(q, keys + long(t) * sc.D, sc.D) * sc.scale;
+      rowScores[t] = v;
+      if (scores) scores[t] = v;
+    }
+  }
+  __syncthreads();
+  const int rowThreads = a.softmax.rowThreads;
+  softmax_row(a.softmax, rowScores, bh, int(threadIdx.x) % rowThreads, int(threadIdx.x) < rowThreads, rowScores);
+  __syncthreads();
+  attention_values_row(a.values, bh, rowScores);
+}
+CKL_ENTRY_ATTR(attention_scores__softmax__attention_values, AttentionChainArgs,
+               attention_scores__softmax__attention_values_body, kValuesBlock, )
 
 // ------------------------------------------------------------------ pointwise
 // add: dst = x + y; multiply: dst = x * y; silu: dst = v / (1 + exp(-v)) (workloads.py:145-167).

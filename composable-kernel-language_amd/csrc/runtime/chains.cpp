@@ -4,12 +4,14 @@
 // most of the time of the decode step's row-local kernels. The kernel library therefore has chain
 // entry points (csrc/kernels/library.hip) that run several dependent dispatches row by row in one
 // grid: rms_stats -> rms_apply, add -> rms_stats -> rms_apply, embedding -> rms_stats ->
-// rms_apply, silu -> multiply and softmax -> attention_values. The plan itself (nodes, edges,
+// rms_apply, silu -> multiply, attention_scores -> softmax -> attention_values (or softmax ->
+// attention_values) and rope(q), rope(k) -> append_kv. The plan itself (nodes, edges,
 // argument blocks) is unchanged; only the inferred lowering contracts a chain into one unit.
 //
 // A chain is taken only when
-//   * each member depends directly on the previous one and the members' entry points and the
-//     chain entry point come from one code object;
+//   * each member depends directly on the previous one (the two ropes of the rope chain are
+//     independent of each other) and the members' entry points and the chain entry point come
+//     from one code object;
 //   * the members' argument blocks agree (the buffer one member writes is the one the next
 //     reads, same shapes), read through the argument structs in csrc/kernels/args.h;
 //   * every buffer range a member writes is disjoint from every other range of the chain, or
@@ -81,6 +83,8 @@ template <typename T> T block(const Launch &launch) {
   std::memcpy(&value, launch.arguments.data(), sizeof(T));
   return value;
 }
+
+bool singleGrid(const Launch &l) { return l.grid[1] == 1 && l.grid[2] == 1 && l.block[1] == 1 && l.block[2] == 1; }
 
 constexpr const char *kOverlap = "buffers overlap in a way row-by-row execution would change";
 
@@ -204,10 +208,111 @@ const char *softmaxValuesChain(const Members &m, const Internal &internal, Launc
   return nullptr;
 }
 
+Range slab(const void *p, uint64_t bytes, bool written) {
+  uint64_t a = reinterpret_cast<uint64_t>(p);
+  return {a, a + bytes, written, false, 0};
+}
+
+const char *attentionChain(const Members &m, const Internal &internal, Launch &out) {
+  AttentionChainArgs c{block<ScoresArgs>(*m[0]), block<SoftmaxArgs>(*m[1]), block<ValuesArgs>(*m[2])};
+  const ScoresArgs &sc = c.scores;
+  const SoftmaxArgs &x = c.softmax;
+  const ValuesArgs &v = c.values;
+  const Launch &values = *m[2];
+  if (sc.scores != x.scores || x.probs != v.probs || sc.position != x.position || x.position != v.position)
+    return "softmax and attention_values do not consume the scores chain";
+  if (sc.B != x.B || sc.A != x.A || sc.T != x.T || x.B != v.B || x.A != v.A || x.T != v.T || sc.D != v.D)
+    return "attention shapes disagree";
+  if (x.B <= 0 || x.A <= 0 || x.T <= 0 || x.T > kChainSoftmaxRow || v.D <= 0 || v.layer < 0 || sc.layer < 0)
+    return "attention row does not fit the chain's LDS copy";
+  if ((x.rowThreads != 64 && x.rowThreads != 256) || values.block[0] < unsigned(x.rowThreads))
+    return "attention_values workgroup is narrower than a softmax row";
+  if (values.grid[0] != unsigned(x.B) * unsigned(x.A)) return "attention_values grid is not one workgroup per row";
+  uint64_t bh = uint64_t(x.B) * uint64_t(x.A), row = 4ull * uint64_t(x.T), head = 4ull * uint64_t(v.D);
+  uint64_t cache = bh * uint64_t(x.T) * uint64_t(v.D);
+  if (internal(0, sc.scores)) c.scores.scores = nullptr;
+  if (internal(1, x.probs)) c.softmax.probs = nullptr;
+  std::vector<Range> ranges{rows(sc.q, bh, head, false), whole(x.position, 4),
+                            whole(sc.kc + int64_t(sc.layer) * int64_t(cache), 4 * cache),
+                            whole(v.vc + int64_t(v.layer) * int64_t(cache), 4 * cache), rows(v.dst, bh, head, true)};
+  if (c.scores.scores) ranges.push_back(rows(sc.scores, bh, row, true));
+  if (c.softmax.probs) ranges.push_back(rows(x.probs, bh, row, true));
+  if (!hazardFree(ranges)) return kOverlap;
+  out.grid[0] = values.grid[0];
+  out.block[0] = values.block[0];
+  out.shared = unsigned(row);
+  setArguments(out, c);
+  return nullptr;
+}
+
+const char *ropeAppendChain(const Members &m, const Internal &internal, Launch &out) {
+  RopeAppendChainArgs c{block<RopeArgs>(*m[0]), block<RopeArgs>(*m[1]), block<AppendArgs>(*m[2])};
+  const RopeArgs &q = c.q, &k = c.k;
+  const AppendArgs &ap = c.append;
+  if (q.table != k.table || q.position != k.position || q.position != ap.position || q.B != k.B || q.A != k.A ||
+      q.R != k.R || q.T != k.T)
+    return "the two ropes disagree on table, position or shape";
+  if (ap.k != k.dst || ap.B != q.B || ap.A != q.A || ap.D != 2 * q.R || ap.T != q.T || ap.layer < 0 || ap.L <= ap.layer)
+    return "append_kv does not take the rotated k";
+  if (q.B <= 0 || q.A <= 0 || q.R <= 0 || q.T <= 0) return "empty rope";
+  uint64_t pairs = uint64_t(q.B) * uint64_t(q.A) * uint64_t(q.R);
+  uint64_t cache = uint64_t(ap.B) * uint64_t(ap.A) * uint64_t(ap.T) * uint64_t(ap.D);
+  if (internal(1, k.dst)) c.k.dst = nullptr;
+  std::vector<Range> ranges{rows(q.src, pairs, 8, false), rows(q.dst, pairs, 8, true), rows(k.src, pairs, 8, false),
+                            rows(ap.v, pairs, 8, false), whole(q.table, 8ull * uint64_t(q.T) * uint64_t(q.R)),
+                            whole(q.position, 4), slab(ap.kc + int64_t(ap.layer) * int64_t(cache), 4 * cache, true),
+                            slab(ap.vc + int64_t(ap.layer) * int64_t(cache), 4 * cache, true)};
+  if (c.k.dst) ranges.push_back(rows(k.dst, pairs, 8, true));
+  if (!hazardFree(ranges)) return kOverlap;
+  out.grid[0] = cdiv(pairs, 256);
+  out.block[0] = 256;
+  out.shared = 0;
+  setArguments(out, c);
+  return nullptr;
+}
+
+using Successors = std::vector<std::vector<size_t>>;
+using Matcher = std::vector<size_t> (*)(const Plan &, size_t head, const Successors &, const std::vector<bool> &taken);
+
+// rope(q), rope(k) -> append_kv: the ropes are independent; append_kv takes the rotated k. The
+// head may be either rope; the other is the nearest untaken rope (roles: q, k, append).
+std::vector<size_t> matchRopeAppend(const Plan &plan, size_t head, const Successors &successors,
+                                    const std::vector<bool> &taken) {
+  const size_t n = plan.nodes.size();
+  auto isRope = [&](size_t k) { return !taken[k] && plan.nodes[k].launch.name == "ckl_rope" && singleGrid(plan.nodes[k].launch); };
+  auto appendOf = [&](size_t rope) {
+    for (size_t s : successors[rope]) {
+      const Launch &l = plan.nodes[s].launch;
+      if (taken[s] || l.name != "ckl_append_kv" || !singleGrid(l)) continue;
+      if (block<AppendArgs>(l).k == block<RopeArgs>(plan.nodes[rope].launch).dst) return s;
+    }
+    return n;
+  };
+  auto nearest = [&](auto accept) {
+    size_t best = n;
+    for (size_t k = 0; k < n; ++k)
+      if (k != head && isRope(k) && accept(k) &&
+          (best == n || (k > head ? k - head : head - k) < (best > head ? best - head : head - best)))
+        best = k;
+    return best;
+  };
+  if (!isRope(head)) return {};
+  size_t append = appendOf(head);
+  if (append != n) {
+    size_t q = nearest([&](size_t) { return true; });
+    if (q == n) return {};
+    return {q, head, append};
+  }
+  size_t k = nearest([&](size_t r) { return appendOf(r) != n; });
+  if (k == n) return {};
+  return {head, k, appendOf(k)};
+}
+
 struct Rule {
-  std::vector<std::string> members;   // entry points, in dependency order
+  std::vector<std::string> members;   // entry points, in role order (dependency order for a path)
   const char *entry;                  // chain entry point
   const char *(*build)(const Members &, const Internal &, Launch &);   // null, or why not
+  Matcher match = nullptr;            // null: each member is a direct successor of the previous
 };
 
 const std::vector<Rule> &rules() {
@@ -216,12 +321,13 @@ const std::vector<Rule> &rules() {
       {{"ckl_embedding", "ckl_rms_stats", "ckl_rms_apply"}, "ckl_embedding__rms_stats__rms_apply", embeddingRmsChain},
       {{"ckl_rms_stats", "ckl_rms_apply"}, "ckl_rms_stats__rms_apply", rmsChain},
       {{"ckl_silu", "ckl_multiply"}, "ckl_silu__multiply", siluMultiplyChain},
+      {{"ckl_attention_scores", "ckl_softmax", "ckl_attention_values"}, "ckl_attention_scores__softmax__attention_values",
+       attentionChain},
       {{"ckl_softmax", "ckl_attention_values"}, "ckl_softmax__attention_values", softmaxValuesChain},
+      {{"ckl_rope", "ckl_rope", "ckl_append_kv"}, "ckl_rope__rope__append_kv", ropeAppendChain, matchRopeAppend},
   };
   return table;
 }
-
-bool singleGrid(const Launch &l) { return l.grid[1] == 1 && l.grid[2] == 1 && l.block[1] == 1 && l.block[2] == 1; }
 
 // Kahn's algorithm over the units given by `unit` (node -> unit id).
 bool acyclic(const Plan &plan, const std::vector<size_t> &unit, size_t units) {
@@ -273,20 +379,33 @@ std::vector<Chain> findChains(const Plan &plan, const std::vector<bool> &tempora
     const Launch &first = plan.nodes[head].launch;
     for (const Rule &rule : rules()) {
       if (first.name != rule.members[0] || !first.module || !singleGrid(first)) continue;
-      std::vector<size_t> members{head};
-      for (size_t k = 1; k < rule.members.size(); ++k) {
-        size_t found = n;
-        for (size_t s : successors[members.back()]) {
-          const Launch &l = plan.nodes[s].launch;
-          if (!taken[s] && l.name == rule.members[k] && l.module == first.module && singleGrid(l) && s < found) found = s;
+      std::vector<size_t> roles;
+      if (rule.match) {
+        roles = rule.match(plan, head, successors, taken);
+        bool same = roles.size() == rule.members.size();
+        for (size_t k = 0; same && k < roles.size(); ++k) same = plan.nodes[roles[k]].launch.module == first.module;
+        if (!same) {
+          trace(head, rule, "its members are not all present");
+          continue;
         }
-        if (found == n) break;
-        members.push_back(found);
+      } else {
+        roles.push_back(head);
+        for (size_t k = 1; k < rule.members.size(); ++k) {
+          size_t found = n;
+          for (size_t s : successors[roles.back()]) {
+            const Launch &l = plan.nodes[s].launch;
+            if (!taken[s] && l.name == rule.members[k] && l.module == first.module && singleGrid(l) && s < found) found = s;
+          }
+          if (found == n) break;
+          roles.push_back(found);
+        }
+        if (roles.size() != rule.members.size()) {
+          trace(head, rule, ("no dependent " + rule.members[roles.size()] + " follows").c_str());
+          continue;
+        }
       }
-      if (members.size() != rule.members.size()) {
-        trace(head, rule, ("no dependent " + rule.members[members.size()] + " follows").c_str());
-        continue;
-      }
+      std::vector<size_t> members = roles;
+      std::sort(members.begin(), members.end());
       hipFunction_t function = nullptr, group = nullptr;
       if (hipModuleGetFunction(&function, first.module, rule.entry) != hipSuccess) {
         (void)hipGetLastError();
@@ -303,7 +422,7 @@ std::vector<Chain> findChains(const Plan &plan, const std::vector<bool> &tempora
       // never share storage); internal when each is a temporary no other dispatch takes.
       auto internal = [&](size_t index, const void *p) {
         std::vector<int64_t> ids;
-        const Launch &l = plan.nodes[members.at(index)].launch;
+        const Launch &l = plan.nodes[roles.at(index)].launch;
         for (size_t slot = 0; slot < l.slotOffsets.size() && slot < l.slotResources.size(); ++slot) {
           uint64_t word = 0;
           if (l.slotResources[slot] < 0 || l.slotOffsets[slot] + 8 > l.arguments.size()) continue;
@@ -321,7 +440,7 @@ std::vector<Chain> findChains(const Plan &plan, const std::vector<bool> &tempora
         return true;
       };
       std::vector<const Launch *> launches;
-      for (size_t m : members) launches.push_back(&plan.nodes[m].launch);
+      for (size_t m : roles) launches.push_back(&plan.nodes[m].launch);
       Launch fused;
       fused.name = rule.entry;
       fused.module = first.module;

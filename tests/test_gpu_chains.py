@@ -1,5 +1,5 @@
 """Library chains in the inferred graph (csrc/runtime/chains.cpp): contracted launches leave exactly
-the state the ordinary launches leave, bit for bit, the decode step runs in 11 launches per layer
+the state the ordinary launches leave, bit for bit, the decode step runs in 9 launches per layer
 plus 4, and a chain whose buffers overlap in a way row-by-row execution would change runs unfused."""
 import numpy as np
 import pytest
@@ -19,9 +19,9 @@ ODD = Config(batch=2, hidden=42, heads=3, layers=2, ffn=31, vocab=70, context=5,
 
 
 def chained_launches(layers):
-    # embedding+rms; per layer: QKV, rope pair, append, scores, softmax+values, O, add+rms,
+    # embedding+rms; per layer: QKV, rope pair+append, scores+softmax+values, O, add+rms,
     # gate/up, silu+multiply, down, add+rms; then lm head, greedy, advance.
-    return 1 + 11 * layers + 3
+    return 1 + 9 * layers + 3
 
 
 @pytest.mark.parametrize("config", [CONFIGS["small"], REFERENCE_SMALL, AWKWARD, ODD],
@@ -33,12 +33,7 @@ def test_chained_graph_is_bit_identical_to_ordinary(device, config):
     reference = oracle.expected(initial, c, c.steps)
     for reuse, inv in session.invocations.items():
         launches = inv.launch_count(mode="graph", batch_size=1)
-        if reuse:
-            # Storage reuse may place attention's output over the scores it is computed from;
-            # that softmax -> attention_values chain then runs as two launches.
-            assert chained_launches(c.layers) <= launches <= chained_launches(c.layers) + c.layers
-        else:
-            assert launches == chained_launches(c.layers)
+        assert launches == chained_launches(c.layers)
         assert inv.launch_count(mode="graph", batch_size=c.steps) == c.steps * launches
         results = {}
         for mode, group in (("ordinary", 1), ("graph", 1), ("graph", c.steps)):
