@@ -36,11 +36,31 @@ struct CKL_ALIGN RmsStatsArgs { const float *x; float *inv; float eps; int B, C;
 // dst[b, c] = x[b, c] * inv[b] * gain[layer, c]   (workloads.py:52-58)
 struct CKL_ALIGN RmsApplyArgs { const float *x; const float *inv; const float *gain; float *dst; int B, C, layer; };
 // dst[b, o] = sum_i x[b, i] * w[layer, i, o]   (workloads.py:61-69)
+// With kSplit > 1 the reduction is split over workgroups that leave partial planes in the
+// workspace; `deferred` = 0: the last workgroup of a tile adds them into dst; 1 (set by the
+// executor, see PartialSource): dst is not written and the consumer adds the planes.
 struct CKL_ALIGN LinearArgs {
   const float *x; const float *w; float *dst; int B, I, O, layer;
-  int tilesN, kSplit, kChunk, pad;
+  int tilesN, kSplit, kChunk, deferred;
   unsigned char *workspace;
 };
+
+// Workspace layout of the linear family: kLinearZeroPage bytes that stay zero (padding loads read
+// them), the split completion counters (uint32 per output tile, padded to 256 B), then the
+// partial planes float[kSplit][rows][O], rows = B for the vector path (ckl_linear_rowvec) and
+// 32 * ceil(B / 32) for the MFMA paths.
+constexpr int kLinearZeroPage = 256;
+constexpr uint64_t linearCounterBytes(uint64_t counters) { return (counters * 4 + 255) & ~uint64_t(255); }
+constexpr uint64_t linearPlaneRows(int B, bool vector) { return vector ? uint64_t(B) : uint64_t((B + 31) / 32) * 32; }
+constexpr uint64_t linearPartialsOffset(int B, int tilesN, bool vector) {
+  return kLinearZeroPage + linearCounterBytes(uint64_t(vector ? B : (B + 31) / 32) * uint64_t(tilesN));
+}
+
+// A consumer operand that is the sum of a split linear's partial planes (the linear's combine
+// deferred to its consumer): value[i] = sum over g < parts of partials[g * planeStride + i], added
+// in g order starting from 0 as the linear's own combine does. parts == 0: read the operand's
+// own pointer.
+struct CKL_ALIGN PartialSource { const float *partials; int64_t planeStride; int parts, pad; };
 // adjacent-pair rotation at the current position   (workloads.py:72-85)
 struct CKL_ALIGN RopeArgs { const float *src; const float *table; const int *position; float *dst; int B, A, R, T; };
 // kc/vc[layer, b, h, p, :] = k/v[b, h*D : h*D+D]   (workloads.py:88-97)
@@ -66,12 +86,12 @@ struct CKL_ALIGN UpdateArgs { const float *src; float *dst; float bias; int n; }
 
 // Chains (member blocks back to back, in dispatch order).
 struct CKL_ALIGN RmsChainArgs { RmsStatsArgs stats; RmsApplyArgs apply; };
-struct CKL_ALIGN AddRmsChainArgs { BinaryArgs add; RmsStatsArgs stats; RmsApplyArgs apply; };
+struct CKL_ALIGN AddRmsChainArgs { BinaryArgs add; RmsStatsArgs stats; RmsApplyArgs apply; PartialSource x, y; };
 struct CKL_ALIGN EmbeddingRmsChainArgs { EmbeddingArgs embedding; RmsStatsArgs stats; RmsApplyArgs apply; };
-struct CKL_ALIGN SiluMultiplyChainArgs { UnaryArgs silu; BinaryArgs multiply; };
+struct CKL_ALIGN SiluMultiplyChainArgs { UnaryArgs silu; BinaryArgs multiply; PartialSource src, y; };
 struct CKL_ALIGN SoftmaxValuesChainArgs { SoftmaxArgs softmax; ValuesArgs values; };
 struct CKL_ALIGN AttentionChainArgs { ScoresArgs scores; SoftmaxArgs softmax; ValuesArgs values; };
-struct CKL_ALIGN RopeAppendChainArgs { RopeArgs q; RopeArgs k; AppendArgs append; };
+struct CKL_ALIGN RopeAppendChainArgs { RopeArgs q; RopeArgs k; AppendArgs append; PartialSource qsrc, ksrc, v; };
 
 // Largest row (in floats) an attention chain keeps in LDS.
 constexpr int kChainSoftmaxRow = 8192;

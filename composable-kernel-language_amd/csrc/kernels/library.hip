@@ -94,6 +94,37 @@ __device__ __forceinline__ void wave_argmax(float &v, int &i) {
 
 __device__ __forceinline__ int load_position(const int *position) { return *position; }
 
+// Operands of chain kernels that may be a split linear's partial planes (PartialSource, args.h):
+// the planes are added in g order starting from 0, as the linear's own combine (split_finish)
+// does, so deferring the combine leaves every value bit-identical. `i` is the element index.
+__device__ __forceinline__ float source1(const PartialSource &src, const float *own, long i) {
+  if (src.parts == 0) return own[i];
+  float t = 0.f;
+#pragma unroll 4
+  for (int g = 0; g < src.parts; ++g) t += src.partials[g * src.planeStride + i];
+  return t;
+}
+__device__ __forceinline__ float2 source2(const PartialSource &src, const float *own, long i) {
+  if (src.parts == 0) return *reinterpret_cast<const float2 *>(own + i);
+  float2 t = make_float2(0.f, 0.f);
+#pragma unroll 4
+  for (int g = 0; g < src.parts; ++g) {
+    float2 v = *reinterpret_cast<const float2 *>(src.partials + g * src.planeStride + i);
+    t.x += v.x; t.y += v.y;
+  }
+  return t;
+}
+__device__ __forceinline__ float4 source4(const PartialSource &src, const float *own, long i) {
+  if (src.parts == 0) return *reinterpret_cast<const float4 *>(own + i);
+  float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 4
+  for (int g = 0; g < src.parts; ++g) {
+    float4 v = *reinterpret_cast<const float4 *>(src.partials + g * src.planeStride + i);
+    t.x += v.x; t.y += v.y; t.z += v.z; t.w += v.w;
+  }
+  return t;
+}
+
 // ------------------------------------------------------------------ embedding
 // dst[b, c] = table[tokens[b], c]   (workloads.py:33-39)
 __device__ void embedding_body(const EmbeddingArgs &a, int block) {
@@ -116,7 +147,7 @@ __device__ void embedding_body(const EmbeddingArgs &a, int block) {
 CKL_ENTRY(embedding, EmbeddingArgs, embedding_body)
 
 // ------------------------------------------------------------------ rms_stats
-// inv[b] = rsqrt(sum_c x[b,c]^2 / C + eps)   (workloads.py:42-49); one wave per row. The squares
+// inv[b] = rsqrt(sum_c x[b,c]^2 / C + eps)   (workloads.py:42-49). The squares
 // are accumulated with explicit FMAs, so the row chains below (which compute the same row sums
 // from the values they produce) round exactly as this kernel does.
 __device__ __forceinline__ float add_squares(float total, float4 v) {
@@ -128,20 +159,31 @@ __device__ __forceinline__ float add_squares(float total, float4 v) {
 __device__ __forceinline__ float rms_inverse(float total, int C, float eps) {
   return 1.0f / __fsqrt_rn(total / float(C) + eps);
 }
+// Sum over the 256 threads of a workgroup: wave sums, then the four wave sums in order.
+__device__ __forceinline__ float block_sum(float v) {
+  __shared__ float waves[kBlock / 64];
+  v = wave_sum(v);
+  if ((threadIdx.x & 63) == 0) waves[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return (waves[0] + waves[1]) + (waves[2] + waves[3]);
+}
+// One 256-thread workgroup per row: thread t accumulates elements t, t+256, ... (float4 when
+// C % 4 == 0) with explicit FMAs, then block_sum. The row chains below use the same order.
 __device__ void rms_stats_body(const RmsStatsArgs &a, int block) {
-  int lane = threadIdx.x & 63;
-  int row = block * (kBlock / 64) + (threadIdx.x >> 6);
+  const int row = block;
   if (row >= a.B) return;
   const float *x = a.x + long(row) * a.C;
   float total = 0.f;
   if ((a.C & 3) == 0) {
     const float4 *x4 = reinterpret_cast<const float4 *>(x);
-    for (int c = lane; c < a.C / 4; c += 64) total = add_squares(total, x4[c]);
+#pragma unroll 4
+    for (int c = threadIdx.x; c < a.C / 4; c += kBlock) total = add_squares(total, x4[c]);
   } else {
-    for (int c = lane; c < a.C; c += 64) total = __builtin_fmaf(x[c], x[c], total);
+#pragma unroll 4
+    for (int c = threadIdx.x; c < a.C; c += kBlock) total = __builtin_fmaf(x[c], x[c], total);
   }
-  total = wave_sum(total);
-  if (lane == 0) a.inv[row] = rms_inverse(total, a.C, a.eps);
+  total = block_sum(total);
+  if (threadIdx.x == 0) a.inv[row] = rms_inverse(total, a.C, a.eps);
 }
 CKL_ENTRY(rms_stats, RmsStatsArgs, rms_stats_body)
 
@@ -170,77 +212,80 @@ __device__ void rms_apply_body(const RmsApplyArgs &a, int block) {
 CKL_ENTRY(rms_apply, RmsApplyArgs, rms_apply_body)
 
 // ------------------------------------------------------------------ row chains ending in rms
-// [producer ->] rms_stats -> rms_apply as one launch of rms_stats's geometry (one wave per row):
-// the wave produces its row (embedding gather or residual add, written to the producer's dst),
-// sums the squares of the values it produced, writes inv[row] (unless the executor cleared the
-// pointer because nothing outside the chain reads inv), then scales the row. Each lane
-// touches the same elements in every phase, so it only reads back its own writes. The executor
-// runs a chain only when its buffers are pairwise disjoint or identical (csrc/runtime/chains.cpp).
-// Per element the arithmetic is that of the separate kernels, so results are bit-identical.
+// [producer ->] rms_stats -> rms_apply as one launch of rms_stats's geometry (one 256-thread
+// workgroup per row): the workgroup produces its row (embedding gather or residual add, written to
+// the producer's dst), sums the squares of the values it produced in rms_stats's order, writes
+// inv[row] (unless the executor cleared the pointer because nothing outside the chain reads inv),
+// then scales the row. Each thread touches the same elements in every phase, so it only reads
+// back its own writes. The executor runs a chain only when its buffers are pairwise disjoint or
+// identical (csrc/runtime/chains.cpp). Per element the arithmetic is that of the separate
+// kernels, so results are bit-identical.
 __device__ __forceinline__ void rms_finish_row(const RmsStatsArgs &stats, const RmsApplyArgs &apply, int row,
-                                               float total, int lane) {
-  total = wave_sum(total);
+                                               float total) {
+  total = block_sum(total);
   const float s = rms_inverse(total, stats.C, stats.eps);
-  if (lane == 0 && stats.inv) stats.inv[row] = s;   // null: only the chain reads inv
+  if (threadIdx.x == 0 && stats.inv) stats.inv[row] = s;   // null: only the chain reads inv
   const int C = apply.C;
   const float *gain = apply.gain + long(apply.layer) * C;
   const float *x = apply.x + long(row) * C;
   float *dst = apply.dst + long(row) * C;
   if ((C & 3) == 0) {
-    for (int c = lane; c < C / 4; c += 64)
+#pragma unroll 4
+    for (int c = threadIdx.x; c < C / 4; c += kBlock)
       reinterpret_cast<float4 *>(dst)[c] = rms_scale(reinterpret_cast<const float4 *>(x)[c], s,
                                                      reinterpret_cast<const float4 *>(gain)[c]);
   } else {
-    for (int c = lane; c < C; c += 64) dst[c] = x[c] * s * gain[c];
+#pragma unroll 4
+    for (int c = threadIdx.x; c < C; c += kBlock) dst[c] = x[c] * s * gain[c];
   }
 }
 
 __device__ void rms_stats__rms_apply_body(const RmsChainArgs &a, int block) {
-  const int lane = threadIdx.x & 63;
-  const int row = block * (kBlock / 64) + (threadIdx.x >> 6);
+  const int row = block;
   if (row >= a.stats.B) return;
   const int C = a.stats.C;
   const float *x = a.stats.x + long(row) * C;
   float total = 0.f;
   if ((C & 3) == 0) {
-    for (int c = lane; c < C / 4; c += 64) total = add_squares(total, reinterpret_cast<const float4 *>(x)[c]);
+#pragma unroll 4
+    for (int c = threadIdx.x; c < C / 4; c += kBlock) total = add_squares(total, reinterpret_cast<const float4 *>(x)[c]);
   } else {
-    for (int c = lane; c < C; c += 64) total = __builtin_fmaf(x[c], x[c], total);
+#pragma unroll 4
+    for (int c = threadIdx.x; c < C; c += kBlock) total = __builtin_fmaf(x[c], x[c], total);
   }
-  rms_finish_row(a.stats, a.apply, row, total, lane);
+  rms_finish_row(a.stats, a.apply, row, total);
 }
 CKL_ENTRY(rms_stats__rms_apply, RmsChainArgs, rms_stats__rms_apply_body)
 
 __device__ void add__rms_stats__rms_apply_body(const AddRmsChainArgs &a, int block) {
-  const int lane = threadIdx.x & 63;
-  const int row = block * (kBlock / 64) + (threadIdx.x >> 6);
+  const int row = block;
   if (row >= a.stats.B) return;
   const int C = a.stats.C;
   const long base = long(row) * C;
   float total = 0.f;
   if ((C & 3) == 0) {
-    const float4 *x = reinterpret_cast<const float4 *>(a.add.x + base), *y = reinterpret_cast<const float4 *>(a.add.y + base);
     float4 *dst = reinterpret_cast<float4 *>(a.add.dst + base);
-    for (int c = lane; c < C / 4; c += 64) {
-      float4 u = x[c], w = y[c];
+#pragma unroll 4
+    for (int c = threadIdx.x; c < C / 4; c += kBlock) {
+      float4 u = source4(a.x, a.add.x, base + 4 * c), w = source4(a.y, a.add.y, base + 4 * c);
       float4 v = make_float4(u.x + w.x, u.y + w.y, u.z + w.z, u.w + w.w);
       dst[c] = v;
       total = add_squares(total, v);
     }
   } else {
-    for (int c = lane; c < C; c += 64) {
-      float v = a.add.x[base + c] + a.add.y[base + c];
+#pragma unroll 4
+    for (int c = threadIdx.x; c < C; c += kBlock) {
+      float v = source1(a.x, a.add.x, base + c) + source1(a.y, a.add.y, base + c);
       a.add.dst[base + c] = v;
       total = __builtin_fmaf(v, v, total);
     }
   }
-  rms_finish_row(a.stats, a.apply, row, total, lane);
+  rms_finish_row(a.stats, a.apply, row, total);
 }
 CKL_ENTRY(add__rms_stats__rms_apply, AddRmsChainArgs, add__rms_stats__rms_apply_body)
 
 __device__ void embedding__rms_stats__rms_apply_body(const EmbeddingRmsChainArgs &a, int block) {
-  const int lane = threadIdx.x & 63;
-  const int row = block * (kBlock / 64) + (threadIdx.x >> 6);
+  const int row = block;
   if (row >= a.stats.B) return;
   const EmbeddingArgs &e = a.embedding;
   const int C = e.C;
@@ -251,19 +296,21 @@ __device__ void embedding__rms_stats__rms_apply_body(const EmbeddingRmsChainArgs
   if ((C & 3) == 0) {
     const float4 *table = reinterpret_cast<const float4 *>(e.table + long(valid ? token : 0) * C);
     float4 *dst = reinterpret_cast<float4 *>(e.dst + long(row) * C);
-    for (int c = lane; c < C / 4; c += 64) {
+#pragma unroll 4
+    for (int c = threadIdx.x; c < C / 4; c += kBlock) {
       float4 v = valid ? table[c] : make_float4(nan, nan, nan, nan);
       dst[c] = v;
       total = add_squares(total, v);
     }
   } else {
-    for (int c = lane; c < C; c += 64) {
+#pragma unroll 4
+    for (int c = threadIdx.x; c < C; c += kBlock) {
       float v = valid ? e.table[long(token) * C + c] : nan;
       e.dst[long(row) * C + c] = v;
       total = __builtin_fmaf(v, v, total);
     }
   }
-  rms_finish_row(a.stats, a.apply, row, total, lane);
+  rms_finish_row(a.stats, a.apply, row, total);
 }
 CKL_ENTRY(embedding__rms_stats__rms_apply, EmbeddingRmsChainArgs, embedding__rms_stats__rms_apply_body)
 
@@ -294,16 +341,15 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 // operations of the wave, stores included, have completed.
 constexpr int kWaitStores = 0x0F70;
 
-// Workspace layout of the linear family: kZeroPage bytes that stay zero (loads of padding read
-// here, so they need neither a predicate nor a select on the loaded value), then the split
-// completion counters (padded to 256 B), then the partial tiles.
-constexpr int kZeroPage = 256;
-__device__ __forceinline__ int counter_bytes(int count) { return (count * 4 + 255) & ~255; }
+// Workspace layout of the linear family (args.h): kLinearZeroPage bytes that stay zero (loads of
+// padding read here, so they need neither a predicate nor a select on the loaded value), then the
+// split completion counters, then the partial planes.
+constexpr int kZeroPage = kLinearZeroPage;
 __device__ __forceinline__ unsigned *split_counters(const LinearArgs &a) {
   return reinterpret_cast<unsigned *>(a.workspace + kZeroPage);
 }
-__device__ __forceinline__ float *split_partials(const LinearArgs &a, int counters) {
-  return reinterpret_cast<float *>(a.workspace + kZeroPage + counter_bytes(counters));
+__device__ __forceinline__ float *split_partials(const LinearArgs &a, bool vector) {
+  return reinterpret_cast<float *>(a.workspace + linearPartialsOffset(a.B, a.tilesN, vector));
 }
 
 // Cross-workgroup partial tiles live in the workspace and are written and read only with
@@ -416,7 +462,77 @@ template <int J, int S> __device__ __forceinline__ void mfma_compute(const MfmaS
       for (int j = 0; j < J; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(st.x[u][i], st.w[u][i][j], acc[j], 0, 0, 0);
 }
 
-template <int J, int S> __device__ void linear_mfma(const LinearArgs &a, int block, float *smem) {
+// Split-bf16 flavour: v_mfma_f32_32x32x16_bf16 at 16x the f32 MFMA rate. Every f32 operand is split
+// exactly into three bf16 parts, v = hi + mid + lo (hi = RNE(v), mid = RNE(v - hi), lo = RNE of the
+// rest), and each 16-row K-step accumulates the six products whose magnitude is above 2^-24 of
+// x*w: hi*hi, hi*mid, mid*hi, hi*lo, lo*hi, mid*mid. The dropped terms are below 2^-23 |x*w|,
+// the size of an f32 rounding, and products of bf16 parts are exact in the f32 accumulator. A
+// lane's 8 K values are rows {k + 8u + 4s + i} of the same permuted K order as the f32 flavour
+// (A and B permuted alike leave the dot product unchanged). An infinite hi part (an infinite
+// operand, or one beyond the bf16 range) keeps mid = lo = 0, so infinities propagate as in f32.
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+struct SplitBf16 { unsigned hi[4], mid[4], lo[4]; };
+
+__device__ __forceinline__ unsigned pack_bf16(float a, float b) {
+  bf16x2 v = {(__bf16)a, (__bf16)b};       // v_cvt_pk_bf16_f32: round to nearest even
+  return __builtin_bit_cast(unsigned, v);
+}
+__device__ __forceinline__ float bf16_low(unsigned p) { return __uint_as_float(p << 16); }
+__device__ __forceinline__ float bf16_high(unsigned p) { return __uint_as_float(p & 0xFFFF0000u); }
+
+__device__ __forceinline__ void split_bf16(const float (&v)[8], SplitBf16 &out) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float a = v[2 * e], b = v[2 * e + 1];
+    const unsigned h = pack_bf16(a, b);
+    const float ha = bf16_low(h), hb = bf16_high(h);
+    const float ra = __builtin_isinf(ha) ? 0.f : a - ha, rb = __builtin_isinf(hb) ? 0.f : b - hb;
+    const unsigned m = pack_bf16(ra, rb);
+    out.hi[e] = h;
+    out.mid[e] = m;
+    out.lo[e] = pack_bf16(ra - bf16_low(m), rb - bf16_high(m));
+  }
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(const unsigned (&p)[4]) {
+  return __builtin_bit_cast(bf16x8, make_uint4(p[0], p[1], p[2], p[3]));
+}
+
+template <int J, int S> __device__ __forceinline__ void mfma_compute_bf16(const MfmaStage<J, S> &st, floatx16 (&acc)[J]) {
+#pragma unroll
+  for (int t = 0; t < S; ++t) {
+    float xv[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { xv[i] = st.x[2 * t][i]; xv[4 + i] = st.x[2 * t + 1][i]; }
+    SplitBf16 xs;
+    split_bf16(xv, xs);
+    const bf16x8 xh = as_bf16x8(xs.hi), xm = as_bf16x8(xs.mid), xl = as_bf16x8(xs.lo);
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      float wv[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) { wv[i] = st.w[2 * t][i][j]; wv[4 + i] = st.w[2 * t + 1][i][j]; }
+      SplitBf16 ws;
+      split_bf16(wv, ws);
+      const bf16x8 wh = as_bf16x8(ws.hi), wm = as_bf16x8(ws.mid), wl = as_bf16x8(ws.lo);
+      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xm, wm, acc[j], 0, 0, 0);
+      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xl, wh, acc[j], 0, 0, 0);
+      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh, wl, acc[j], 0, 0, 0);
+      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xm, wh, acc[j], 0, 0, 0);
+      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh, wm, acc[j], 0, 0, 0);
+      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh, wh, acc[j], 0, 0, 0);
+    }
+  }
+}
+
+enum class MfmaFlavour { F32, SplitBf16 };
+template <MfmaFlavour F, int J, int S> __device__ __forceinline__ void stage_compute(const MfmaStage<J, S> &st, floatx16 (&acc)[J]) {
+  if constexpr (F == MfmaFlavour::F32) mfma_compute<J, S>(st, acc);
+  else mfma_compute_bf16<J, S>(st, acc);
+}
+
+template <MfmaFlavour F, int J, int S> __device__ void linear_mfma(const LinearArgs &a, int block, float *smem) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform: scalar loop control
   const int m = lane & 31, s = lane >> 5;
@@ -455,21 +571,21 @@ template <int J, int S> __device__ void linear_mfma(const LinearArgs &a, int blo
   for (; t + 1 < full; t += 2) {
     mfma_load<J, S, false>(sb, xr, w, a.O, k + 4 * R * (t + 1), k1);
     __builtin_amdgcn_sched_barrier(0);
-    mfma_compute<J, S>(sa, acc);
+    stage_compute<F, J, S>(sa, acc);
     __builtin_amdgcn_sched_barrier(0);
     mfma_load<J, S, false>(sa, xr, w, a.O, k + 4 * R * min(t + 2, full - 1), k1);
     __builtin_amdgcn_sched_barrier(0);
-    mfma_compute<J, S>(sb, acc);
+    stage_compute<F, J, S>(sb, acc);
     __builtin_amdgcn_sched_barrier(0);
   }
-  if (t < full) mfma_compute<J, S>(sa, acc);
+  if (t < full) stage_compute<F, J, S>(sa, acc);
   const int tailBase = kb0 + R * fullTotal;
   const int tailStages = (kb1 - tailBase + 15) / 16;
 #pragma unroll 1
   for (int q = (wave - fullTotal % 4 + 4) % 4; q < tailStages; q += 4) {
     MfmaStage<J, 1> st;
     mfma_load<J, 1, true>(st, xr, w, a.O, tailBase + 16 * q + 4 * s, k1);
-    mfma_compute<J, 1>(st, acc);
+    stage_compute<F, J, 1>(st, acc);
   }
 
   // Waves 1..3 hand their tiles to wave 0 through LDS; wave 0 adds them in wave order.
@@ -481,7 +597,7 @@ template <int J, int S> __device__ void linear_mfma(const LinearArgs &a, int blo
   }
   __syncthreads();
   const int rowTiles = (a.B + 31) / 32;
-  float *partial = split_partials(a, rowTiles * a.tilesN);
+  float *partial = split_partials(a, false);
   if (wave == 0) {
 #pragma unroll 1
     for (int v = 1; v < 4; ++v)
@@ -506,7 +622,7 @@ template <int J, int S> __device__ void linear_mfma(const LinearArgs &a, int blo
       }
     }
   }
-  if (a.kSplit > 1) {
+  if (a.kSplit > 1 && !a.deferred) {
     unsigned *counters = split_counters(a);
     if (split_arrive(counters + rt * a.tilesN + tn, a.kSplit, wave))
       split_finish(a, partial, long(rowTiles) * 32 * a.O, rt * 32, 32, tn * 32 * J, 32 * J);
@@ -556,20 +672,24 @@ __device__ void linear_rowvec_body(const LinearArgs &a, int block) {
   red[wave][lane] = acc;
   __syncthreads();
   if (wave != 0 || !colOk) {
-    if (a.kSplit == 1) return;
+    if (a.kSplit == 1 || a.deferred) return;
   } else {
     float v = red[0][lane];
     for (int v2 = 1; v2 < waves; ++v2) v += red[v2][lane];
-    if (a.kSplit > 1) partial_store(split_partials(a, a.B * a.tilesN) + (long(kg) * a.B + b) * a.O + col, v);
+    if (a.kSplit > 1) partial_store(split_partials(a, true) + (long(kg) * a.B + b) * a.O + col, v);
     else a.dst[long(b) * a.O + col] = v;
   }
-  if (a.kSplit > 1 && split_arrive(split_counters(a) + b * a.tilesN + tn, a.kSplit, wave))
-    split_finish(a, split_partials(a, a.B * a.tilesN), long(a.B) * a.O, b, 1, tn * 64, 64);
+  if (a.kSplit > 1 && !a.deferred && split_arrive(split_counters(a) + b * a.tilesN + tn, a.kSplit, wave))
+    split_finish(a, split_partials(a, true), long(a.B) * a.O, b, 1, tn * 64, 64);
 }
 
 template <int J, int S> __device__ void linear_mfma_body(const LinearArgs &a, int block) {
   extern __shared__ float smem[];
-  linear_mfma<J, S>(a, block, smem);
+  linear_mfma<MfmaFlavour::F32, J, S>(a, block, smem);
+}
+template <int J, int S> __device__ void linear_split_body(const LinearArgs &a, int block) {
+  extern __shared__ float smem[];
+  linear_mfma<MfmaFlavour::SplitBf16, J, S>(a, block, smem);
 }
 CKL_ENTRY_ATTR(linear_rowvec, LinearArgs, linear_rowvec_body, 1024, )
 // ckl_linear_mfma<J>x<S>: J weight columns per lane, 16*S reduction rows per stage.
@@ -581,6 +701,13 @@ CKL_ENTRY_ATTR(linear_mfma2x2, LinearArgs, (linear_mfma_body<2, 2>), kBlock, CKL
 CKL_ENTRY_ATTR(linear_mfma2x4, LinearArgs, (linear_mfma_body<2, 4>), kBlock, CKL_TWO_WAVES)
 CKL_ENTRY_ATTR(linear_mfma4x1, LinearArgs, (linear_mfma_body<4, 1>), kBlock, CKL_TWO_WAVES)
 CKL_ENTRY_ATTR(linear_mfma4x2, LinearArgs, (linear_mfma_body<4, 2>), kBlock, CKL_TWO_WAVES)
+// ckl_linear_split<J>x<S>: the same tiling with the split-bf16 MFMA flavour.
+CKL_ENTRY(linear_split1x1, LinearArgs, (linear_split_body<1, 1>))
+CKL_ENTRY(linear_split1x2, LinearArgs, (linear_split_body<1, 2>))
+CKL_ENTRY_ATTR(linear_split2x1, LinearArgs, (linear_split_body<2, 1>), kBlock, CKL_TWO_WAVES)
+CKL_ENTRY_ATTR(linear_split2x2, LinearArgs, (linear_split_body<2, 2>), kBlock, CKL_TWO_WAVES)
+CKL_ENTRY_ATTR(linear_split4x1, LinearArgs, (linear_split_body<4, 1>), kBlock, CKL_TWO_WAVES)
+CKL_ENTRY_ATTR(linear_split4x2, LinearArgs, (linear_split_body<4, 2>), kBlock, CKL_TWO_WAVES)
 
 // ------------------------------------------------------------------ rope
 // Adjacent-pair rotation at position p (workloads.py:72-85):
@@ -648,12 +775,12 @@ __device__ void rope__rope__append_kv_body(const RopeAppendChainArgs &a, int blo
   int h = int(bh % q.A), b = int(bh / q.A);
   long c = long(b) * (2L * q.R * q.A) + long(h) * (2 * q.R) + 2 * r;
   float2 cs = *reinterpret_cast<const float2 *>(q.table + (long(p) * q.R + r) * 2);
-  *reinterpret_cast<float2 *>(q.dst + c) = rotate(*reinterpret_cast<const float2 *>(q.src + c), cs);
-  float2 kr = rotate(*reinterpret_cast<const float2 *>(k.src + c), cs);
+  *reinterpret_cast<float2 *>(q.dst + c) = rotate(source2(a.qsrc, q.src, c), cs);
+  float2 kr = rotate(source2(a.ksrc, k.src, c), cs);
   if (k.dst) *reinterpret_cast<float2 *>(k.dst + c) = kr;
   long row = (((long(ap.layer) * ap.B * ap.A) + bh) * ap.T + p) * ap.D + 2 * r;
   *reinterpret_cast<float2 *>(ap.kc + row) = kr;
-  *reinterpret_cast<float2 *>(ap.vc + row) = *reinterpret_cast<const float2 *>(ap.v + c);
+  *reinterpret_cast<float2 *>(ap.vc + row) = source2(a.v, ap.v, c);
 }
 CKL_ENTRY(rope__rope__append_kv, RopeAppendChainArgs, rope__rope__append_kv_body)
 
@@ -980,16 +1107,16 @@ __device__ void silu__multiply_body(const SiluMultiplyChainArgs &a, int block) {
   const int n = a.silu.n;
   if ((n & 3) == 0) {
     if (i >= n / 4) return;
-    float4 v = reinterpret_cast<const float4 *>(a.silu.src)[i];
+    float4 v = source4(a.src, a.silu.src, 4 * i);
     float4 act = make_float4(silu(v.x), silu(v.y), silu(v.z), silu(v.w));
     if (a.silu.dst) reinterpret_cast<float4 *>(a.silu.dst)[i] = act;   // null: only multiply reads it
-    float4 y = reinterpret_cast<const float4 *>(a.multiply.y)[i];
+    float4 y = source4(a.y, a.multiply.y, 4 * i);
     reinterpret_cast<float4 *>(a.multiply.dst)[i] =
         make_float4(binary<1>(act.x, y.x), binary<1>(act.y, y.y), binary<1>(act.z, y.z), binary<1>(act.w, y.w));
   } else if (i < n) {
-    float act = silu(a.silu.src[i]);
+    float act = silu(source1(a.src, a.silu.src, i));
     if (a.silu.dst) a.silu.dst[i] = act;
-    a.multiply.dst[i] = binary<1>(act, a.multiply.y[i]);
+    a.multiply.dst[i] = binary<1>(act, source1(a.y, a.multiply.y, i));
   }
 }
 CKL_ENTRY(silu__multiply, SiluMultiplyChainArgs, silu__multiply_body)

@@ -27,6 +27,7 @@
 #include "../kernels/args.h"
 
 #include <algorithm>
+#include <cstddef>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -90,9 +91,9 @@ constexpr const char *kOverlap = "buffers overlap in a way row-by-row execution 
 
 unsigned cdiv(uint64_t a, uint64_t b) { return unsigned((a + b - 1) / b); }
 
-// Geometry of the rms chains: one wave per row, four rows per 256-thread workgroup.
+// Geometry of the rms chains: one 256-thread workgroup per row (rms_stats's geometry).
 void rowGeometry(Launch &out, int rowsCount) {
-  out.grid[0] = cdiv(uint64_t(rowsCount), 4);
+  out.grid[0] = unsigned(rowsCount);
   out.block[0] = 256;
   out.shared = 0;
 }
@@ -313,18 +314,25 @@ struct Rule {
   const char *entry;                  // chain entry point
   const char *(*build)(const Members &, const Internal &, Launch &);   // null, or why not
   Matcher match = nullptr;            // null: each member is a direct successor of the previous
+  std::vector<std::array<size_t, 3>> deferrable = {};   // {role, member pointer offset, source offset}
 };
 
 const std::vector<Rule> &rules() {
   static const std::vector<Rule> table = {
-      {{"ckl_add", "ckl_rms_stats", "ckl_rms_apply"}, "ckl_add__rms_stats__rms_apply", addRmsChain},
+      {{"ckl_add", "ckl_rms_stats", "ckl_rms_apply"}, "ckl_add__rms_stats__rms_apply", addRmsChain, nullptr,
+       {{0, offsetof(BinaryArgs, x), offsetof(AddRmsChainArgs, x)}, {0, offsetof(BinaryArgs, y), offsetof(AddRmsChainArgs, y)}}},
       {{"ckl_embedding", "ckl_rms_stats", "ckl_rms_apply"}, "ckl_embedding__rms_stats__rms_apply", embeddingRmsChain},
       {{"ckl_rms_stats", "ckl_rms_apply"}, "ckl_rms_stats__rms_apply", rmsChain},
-      {{"ckl_silu", "ckl_multiply"}, "ckl_silu__multiply", siluMultiplyChain},
+      {{"ckl_silu", "ckl_multiply"}, "ckl_silu__multiply", siluMultiplyChain, nullptr,
+       {{0, offsetof(UnaryArgs, src), offsetof(SiluMultiplyChainArgs, src)},
+        {1, offsetof(BinaryArgs, y), offsetof(SiluMultiplyChainArgs, y)}}},
       {{"ckl_attention_scores", "ckl_softmax", "ckl_attention_values"}, "ckl_attention_scores__softmax__attention_values",
        attentionChain},
       {{"ckl_softmax", "ckl_attention_values"}, "ckl_softmax__attention_values", softmaxValuesChain},
-      {{"ckl_rope", "ckl_rope", "ckl_append_kv"}, "ckl_rope__rope__append_kv", ropeAppendChain, matchRopeAppend},
+      {{"ckl_rope", "ckl_rope", "ckl_append_kv"}, "ckl_rope__rope__append_kv", ropeAppendChain, matchRopeAppend,
+       {{0, offsetof(RopeArgs, src), offsetof(RopeAppendChainArgs, qsrc)},
+        {1, offsetof(RopeArgs, src), offsetof(RopeAppendChainArgs, ksrc)},
+        {2, offsetof(AppendArgs, v), offsetof(RopeAppendChainArgs, v)}}},
   };
   return table;
 }
@@ -460,11 +468,70 @@ std::vector<Chain> findChains(const Plan &plan, const std::vector<bool> &tempora
       trace(head, rule, "taken");
       unit = std::move(trial);
       for (size_t m : members) taken[m] = true;
-      chains.push_back({std::move(members), std::move(fused)});
+      chains.push_back({std::move(members), std::move(fused), roles, rule.deferrable});
       break;
     }
   }
   return chains;
+}
+
+std::map<size_t, Launch> deferCombines(const Plan &plan, const std::vector<bool> &temporary, std::vector<Chain> &chains) {
+  auto slotAt = [](const Launch &l, size_t offset) -> int64_t {
+    for (size_t s = 0; s < l.slotOffsets.size() && s < l.slotResources.size(); ++s)
+      if (l.slotOffsets[s] == offset) return int64_t(s);
+    return -1;
+  };
+  // Deferrable chain operands by the plan resource they read: {chain, source offset, node, slot}.
+  struct Operand { size_t chain, source, node; int64_t slot; };
+  std::map<int64_t, std::vector<Operand>> operands;
+  for (size_t c = 0; c < chains.size(); ++c)
+    for (const auto &[role, pointer, source] : chains[c].deferrable) {
+      size_t node = chains[c].roles.at(role);
+      int64_t slot = slotAt(plan.nodes[node].launch, pointer);
+      if (slot < 0) continue;
+      int64_t resource = plan.nodes[node].launch.slotResources[size_t(slot)];
+      if (resource >= 0) operands[resource].push_back({c, source, node, slot});
+    }
+  std::map<size_t, Launch> patched;
+  for (size_t p = 0; p < plan.nodes.size(); ++p) {
+    const Launch &l = plan.nodes[p].launch;
+    if (l.name.rfind("ckl_linear_", 0) != 0) continue;
+    LinearArgs a = block<LinearArgs>(l);
+    int64_t dstSlot = slotAt(l, offsetof(LinearArgs, dst));
+    if (a.kSplit <= 1 || a.deferred || dstSlot < 0 || !a.workspace) continue;
+    int64_t resource = l.slotResources[size_t(dstSlot)];
+    if (resource < 0 || size_t(resource) >= temporary.size() || !temporary[size_t(resource)]) continue;
+    auto found = operands.find(resource);
+    if (found == operands.end()) continue;
+    // Every other argument taking the resource must be one of the deferrable operands.
+    bool all = true;
+    for (size_t k = 0; k < plan.nodes.size() && all; ++k) {
+      const Launch &consumer = plan.nodes[k].launch;
+      for (size_t s = 0; s < consumer.slotResources.size() && all; ++s) {
+        if (consumer.slotResources[s] != resource || (k == p && int64_t(s) == dstSlot)) continue;
+        bool listed = false;
+        for (const Operand &o : found->second) listed |= o.node == k && o.slot == int64_t(s);
+        all = listed;
+      }
+    }
+    const bool vector = l.name == "ckl_linear_rowvec";
+    const uint64_t stride = linearPlaneRows(a.B, vector) * uint64_t(a.O);
+    if (!all || stride % 4) continue;
+    PartialSource source{reinterpret_cast<const float *>(a.workspace + linearPartialsOffset(a.B, a.tilesN, vector)),
+                         int64_t(stride), a.kSplit, 0};
+    for (const Operand &o : found->second) {
+      std::vector<uint8_t> &bytes = chains[o.chain].launch.arguments;
+      if (o.source + sizeof source > bytes.size()) throw std::logic_error("chain block has no room for a partial source");
+      std::memcpy(bytes.data() + o.source, &source, sizeof source);
+    }
+    Launch deferred = l;
+    a.deferred = 1;
+    std::memcpy(deferred.arguments.data(), &a, sizeof a);
+    if (tracing()) std::fprintf(stderr, "[ckl chains] node %zu %s: combine deferred to %zu readers\n", p, l.name.c_str(),
+                                found->second.size());
+    patched.emplace(p, std::move(deferred));
+  }
+  return patched;
 }
 
 } // namespace ckl::rt

@@ -18,6 +18,11 @@ int deviceCount() {
   return count;
 }
 
+bool inferredOnStream() {
+  const char *value = std::getenv("CKL_INFERRED_STREAM");
+  return value && std::strcmp(value, "1") == 0;
+}
+
 BranchPolicy branchPolicy() {
   const char *value = std::getenv("CKL_GRAPH_BRANCHES");
   return value && std::strcmp(value, "1") == 0 ? BranchPolicy::Branches : BranchPolicy::Grouped;
@@ -192,8 +197,10 @@ Launch groupLaunch(const std::vector<const Launch *> &members) {
 
 // The inferred lowering: library chains are contracted into single units, units are levelled by
 // their longest dependency path, and same-level units of one family become one group launch.
-// `chains` were found on one iteration of `iterations` (the plan's nodes repeat with that period).
-std::vector<Unit> groupPlan(const Plan &plan, const std::vector<Chain> &found, size_t iterations) {
+// `chains` and the patched launches `overrides` were found on one iteration of `iterations` (the
+// plan's nodes repeat with that period).
+std::vector<Unit> groupPlan(const Plan &plan, const std::vector<Chain> &found, const std::map<size_t, Launch> &overrides,
+                            size_t iterations) {
   const size_t n = plan.nodes.size();
   const size_t period = n / iterations;
   std::vector<Chain> chains;
@@ -215,7 +222,8 @@ std::vector<Unit> groupPlan(const Plan &plan, const std::vector<Chain> &found, s
       base.push_back({c.members, c.launch});
     } else {
       unitOf[k] = base.size();
-      base.push_back({{k}, plan.nodes[k].launch});
+      auto patched = overrides.find(k % period);
+      base.push_back({{k}, patched != overrides.end() ? patched->second : plan.nodes[k].launch});
     }
   }
   const size_t units = base.size();
@@ -372,10 +380,13 @@ GraphExec &Invocation::graphFor(int mode, uint64_t batch) {
       slot = explicitGraph(repeated, units);
     } else {
       // Chains contracted, sibling groups ordered by DAG level, captured as one launch chain.
-      std::vector<Unit> units = groupPlan(repeated, findChains(plan, temporaryResources), batch);
+      std::vector<Chain> chains = findChains(plan, temporaryResources);
+      std::map<size_t, Launch> deferred = deferCombines(plan, temporaryResources, chains);
+      std::vector<Unit> units = groupPlan(repeated, chains, deferred, batch);
       std::vector<Launch> launches;
       for (const Unit &u : units) launches.push_back(u.launch);
       slot = captureUnits(launches, stream);
+      slot->launches = std::move(launches);
     }
   }
   return *slot;
@@ -384,7 +395,11 @@ GraphExec &Invocation::graphFor(int mode, uint64_t batch) {
 void Invocation::execute(int mode, uint64_t batch) {
   device->makeCurrent();
   if (mode) {
-    check(hipGraphLaunch(graphFor(mode, batch).exec, stream), "hipGraphLaunch");
+    GraphExec &graph = graphFor(mode, batch);
+    if (mode == 1 && !graph.launches.empty() && inferredOnStream())
+      for (const Launch &l : graph.launches) launchOne(l, stream);
+    else
+      check(hipGraphLaunch(graph.exec, stream), "hipGraphLaunch");
   } else {
     for (uint64_t k = 0; k < batch; ++k) launchOrdinary(plan, stream);
   }

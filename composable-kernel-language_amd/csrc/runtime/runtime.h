@@ -82,16 +82,24 @@ struct Plan {
 // argument blocks back to back. Found on one iteration of the plan; `temporary[id]` tells
 // whether plan resource `id` is a heap temporary (a buffer no caller can observe).
 struct Chain {
-  std::vector<size_t> members;
+  std::vector<size_t> members;                     // ascending plan indices
   Launch launch;
+  std::vector<size_t> roles;                       // members in the chain block's order
+  // Operands that may read a split linear's partial planes: {role, offset of the pointer in the
+  // member's block, offset of its PartialSource in the chain block}.
+  std::vector<std::array<size_t, 3>> deferrable;
 };
 std::vector<Chain> findChains(const Plan &plan, const std::vector<bool> &temporary);
+// Split linears whose every reader is a deferrable chain operand leave their combine to those
+// chains: returns the patched linear launches (by plan index) and fills the chains' sources.
+std::map<size_t, Launch> deferCombines(const Plan &plan, const std::vector<bool> &temporary, std::vector<Chain> &chains);
 
 struct GraphExec {
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
   size_t nodeCount = 0;
   std::vector<std::vector<uint8_t>> storage;   // kernarg blocks referenced during capture
+  std::vector<Launch> launches;                // the captured launch chain (grouped inferred policy)
   ~GraphExec();
 };
 
@@ -160,6 +168,9 @@ std::shared_ptr<Invocation> bind(const std::shared_ptr<ProgramState> &program, s
 // node per dispatch with real branches.
 enum class BranchPolicy { Grouped, Branches };
 BranchPolicy branchPolicy();
+// CKL_INFERRED_STREAM=1: mode 1 issues the grouped inferred launch chain as ordinary stream
+// launches instead of one graph launch (same kernels and order; for per-kernel profiling).
+bool inferredOnStream();
 
 int deviceCount();
 

@@ -244,7 +244,7 @@ def _embedding(shapes, consts, ext):
 
 def _rms_stats(shapes, consts, ext):
     b, c = shapes[0]
-    return Launch(_cdiv(b, 4), (b, c)) if ext[0] >= b and ext[1:] == (1, 1) else None
+    return Launch(b, (b, c)) if ext[0] >= b and ext[1:] == (1, 1) else None      # one workgroup per row
 
 
 def _rms_apply(shapes, consts, ext):

@@ -16,6 +16,10 @@ REFERENCE_SMALL = Config(batch=1, hidden=64, heads=4, layers=2, ffn=128, vocab=2
 AWKWARD = Config(batch=3, hidden=48, heads=3, layers=1, ffn=80, vocab=129, context=3, steps=16)
 # Rows not a multiple of 4 floats (scalar paths of the rms and silu chains), D = 14.
 ODD = Config(batch=2, hidden=42, heads=3, layers=2, ffn=31, vocab=70, context=5, steps=6)
+# Split reductions whose combine the chains take over: MFMA path (B > 16, splits 2 and 3) and
+# vector path (B <= 16, reductions over 1024 rows).
+SPLIT_MFMA = Config(batch=20, hidden=1024, heads=8, layers=1, ffn=1536, vocab=300, context=4, steps=3)
+SPLIT_VECTOR = Config(batch=5, hidden=1280, heads=10, layers=1, ffn=1536, vocab=300, context=4, steps=3)
 
 
 def chained_launches(layers):
@@ -24,8 +28,8 @@ def chained_launches(layers):
     return 1 + 9 * layers + 3
 
 
-@pytest.mark.parametrize("config", [CONFIGS["small"], REFERENCE_SMALL, AWKWARD, ODD],
-                         ids=["small", "reference_small", "awkward", "odd"])
+@pytest.mark.parametrize("config", [CONFIGS["small"], REFERENCE_SMALL, AWKWARD, ODD, SPLIT_MFMA, SPLIT_VECTOR],
+                         ids=["small", "reference_small", "awkward", "odd", "split_mfma", "split_vector"])
 def test_chained_graph_is_bit_identical_to_ordinary(device, config):
     c = config
     initial, _ = oracle.make_inputs(c, 7, init="reference")
