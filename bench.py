@@ -180,33 +180,51 @@ def measured_traffic(config, family):
     return json.loads(path.read_text()).get("families", {}).get(family)
 
 
-def kernel_roofline(session, c, iterations=10):
-    """Time every plan node of one step with HIP events (back-to-back launches of the node on the
-    invocation stream) and return per-family totals and the roofline entry of the dominant family
-    (largest total time per step): algorithmic bytes per launch / average launch duration."""
+def unit_family(name):
+    """Kernel family of an inferred-step launch: the library family of a plain or grouped
+    dispatch ("ckl_linear_mfma1x1_group" -> "linear"), or the chain entry point itself."""
+    name = name[len("ckl_"):] if name.startswith("ckl_") else name
+    name = name[:-len("_group")] if name.endswith("_group") else name
+    return "linear" if name.startswith("linear_") else name
+
+
+def kernel_roofline(session, c, samples=7):
+    """Time every launch of the inferred step (chains contracted, siblings grouped: what the
+    headline mode executes) in sequence on the invocation stream, operands as cold as in a graph
+    replay: launch k's duration is the difference of the median HIP-event times of the step's
+    first k+1 and first k launches (`samples` repeats each). Returns per-family totals and the roofline entry of the dominant family
+    (largest total time per step): algorithmic bytes per launch / average launch duration. A
+    launch's algorithmic bytes are the sum of its plan nodes' (exact for plain and grouped linear
+    launches; for chains this also counts hand-offs kept on chip, a few per cent at most of the
+    attention chain's bytes)."""
     inv = session.invocations[True]
-    session.state.reset()
     position = c.context - 1
     nodes = decoder_node_bytes(c, position)
     if len(nodes) != inv.node_count:
         raise AssertionError("plan does not have the decode program's dispatch count")
+    units = inv.units()
+    session.state.reset(LIGHT_RESET)
+    durations = inv.profile_units(samples)
+    session.state.reset()
     per_kernel = {}
-    for index, (family, algorithmic) in enumerate(nodes):
-        kernel = inv.node_name(index)
-        if not kernel.startswith("ckl_" + family):
-            raise AssertionError(f"plan node {index} is {kernel}, expected the {family} family")
+    for index, (name, members) in enumerate(units):
+        families = {nodes[m][0] for m in members}
+        family = unit_family(name)
+        if family == "linear" and families != {"linear"}:
+            raise AssertionError(f"launch {index} ({name}) runs non-linear plan nodes")
         if family == "advance":
             continue
-        us = inv.time_node(index, iterations)
-        entry = per_kernel.setdefault(family, {"launches": 0, "total_us": 0.0, "bytes": 0, "entries": set()})
+        us = durations[index]
+        entry = per_kernel.setdefault(family, {"launches": 0, "total_us": 0.0, "bytes": 0, "entries": set(), "nodes": 0})
         entry["launches"] += 1
+        entry["nodes"] += len(members)
         entry["total_us"] += us
-        entry["bytes"] += algorithmic
-        entry["entries"].add(kernel)
+        entry["bytes"] += sum(nodes[m][1] for m in members)
+        entry["entries"].add(name)
     session.state.reset()
-    summary = {k: {"launches": v["launches"], "avg_us": v["total_us"] / v["launches"], "total_us": v["total_us"],
-                   "algorithmic_bytes": v["bytes"], "achieved_GBps": v["bytes"] / v["total_us"] / 1e3,
-                   "entry_points": sorted(v["entries"])}
+    summary = {k: {"launches": v["launches"], "plan_nodes": v["nodes"], "avg_us": v["total_us"] / v["launches"],
+                   "total_us": v["total_us"], "algorithmic_bytes": v["bytes"],
+                   "achieved_GBps": v["bytes"] / v["total_us"] / 1e3, "entry_points": sorted(v["entries"])}
                for k, v in sorted(per_kernel.items(), key=lambda kv: -kv[1]["total_us"])}
     dominant = next(iter(summary))
     entry = summary[dominant]
@@ -215,8 +233,8 @@ def kernel_roofline(session, c, iterations=10):
     achieved = per_launch / (avg * 1e-6)
     roofline = {"bound": "hbm", "kernel": f"ckl_{dominant}", "achieved": achieved / 1e9, "peak": HBM_PEAK / 1e9,
                 "unit": "GB/s", "frac": achieved / HBM_PEAK, "traffic": measured_traffic(c_name(c), dominant),
-                "algorithmic_bytes_per_launch": per_launch, "avg_launch_us": avg,
-                "config": c_name(c), "position": position}
+                "algorithmic_bytes_per_launch": per_launch, "avg_launch_us": avg, "launches_per_step": entry["launches"],
+                "config": c_name(c), "position": position, "mode": "inferred step launches in sequence (prefix differences)"}
     return summary, dominant, roofline
 
 
@@ -298,7 +316,7 @@ def main():
         summary, dominant, roofline = kernel_roofline(session, c)
         result["kernels"] = summary
         for family, row in summary.items():
-            log(f"[{name}] {family:18s} launches={row['launches']:3d} avg={row['avg_us']:9.2f} us "
+            log(f"[{name}] {family:38s} launches={row['launches']:3d} avg={row['avg_us']:9.2f} us "
                 f"total={row['total_us']:9.2f} us  {row['achieved_GBps']:8.1f} GB/s")
         if name == "large":
             result["roofline"] = roofline

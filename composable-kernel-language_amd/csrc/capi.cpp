@@ -371,6 +371,54 @@ const char *ckl_invocation_node_name(ckl_invocation *invocation, uint64_t index)
   }
 }
 
+int ckl_invocation_unit_count(ckl_invocation *invocation, uint64_t *count) {
+  return guarded([&] {
+    require(invocation, "invocation");
+    require(count, "count");
+    *count = invocation->invocation->unitCount();
+  });
+}
+
+int ckl_invocation_unit_name(ckl_invocation *invocation, uint64_t unit, const char **name) {
+  return guarded([&] {
+    require(invocation, "invocation");
+    require(name, "name");
+    *name = invocation->invocation->unitName(unit).c_str();
+  });
+}
+
+int ckl_invocation_unit_members(ckl_invocation *invocation, uint64_t unit, uint64_t *members, uint64_t capacity,
+                                uint64_t *count) {
+  return guarded([&] {
+    require(invocation, "invocation");
+    require(count, "count");
+    const auto &list = invocation->invocation->unitMembers(unit);
+    *count = list.size();
+    if (members)
+      for (size_t k = 0; k < list.size() && k < capacity; ++k) members[k] = list[k];
+  });
+}
+
+int ckl_invocation_time_unit(ckl_invocation *invocation, uint64_t unit, uint64_t iterations, double *average_us) {
+  return guarded([&] {
+    require(invocation, "invocation");
+    require(average_us, "average_us");
+    *average_us = invocation->invocation->timeUnit(unit, iterations);
+  });
+}
+
+int ckl_invocation_profile_units(ckl_invocation *invocation, uint64_t repeats, double *durations_us, uint64_t capacity,
+                                 uint64_t *count) {
+  return guarded([&] {
+    require(invocation, "invocation");
+    require(count, "count");
+    std::vector<double> d = invocation->invocation->profileUnits(repeats);
+    *count = d.size();
+    if (durations_us)
+      for (size_t k = 0; k < d.size() && k < capacity; ++k) durations_us[k] = d[k];
+  });
+}
+
 void ckl_invocation_release(ckl_invocation *invocation) { delete invocation; }
 
 } // extern "C"

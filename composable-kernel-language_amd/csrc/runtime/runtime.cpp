@@ -387,6 +387,7 @@ GraphExec &Invocation::graphFor(int mode, uint64_t batch) {
       for (const Unit &u : units) launches.push_back(u.launch);
       slot = captureUnits(launches, stream);
       slot->launches = std::move(launches);
+      for (Unit &u : units) slot->members.push_back(std::move(u.members));
     }
   }
   return *slot;
@@ -455,9 +456,78 @@ std::array<double, 3> Invocation::benchmark(int mode, uint64_t iterations, uint6
 }
 
 double Invocation::timeNode(size_t index, uint64_t iterations) {
-  if (!iterations) throw std::invalid_argument("iterations must be positive");
   std::lock_guard<std::mutex> lock(runMutex);
-  const Launch &launch = plan.nodes.at(index).launch;
+  return timeLaunch(plan.nodes.at(index).launch, iterations);
+}
+
+GraphExec &Invocation::inferredUnits() {
+  if (branchPolicy() != BranchPolicy::Grouped)
+    throw std::invalid_argument("inferred units are defined for the grouped graph policy only");
+  validate(1, 1);
+  return graphFor(1, 1);
+}
+
+size_t Invocation::unitCount() {
+  std::lock_guard<std::mutex> lock(runMutex);
+  return inferredUnits().launches.size();
+}
+
+const std::string &Invocation::unitName(size_t unit) {
+  std::lock_guard<std::mutex> lock(runMutex);
+  return inferredUnits().launches.at(unit).name;
+}
+
+const std::vector<size_t> &Invocation::unitMembers(size_t unit) {
+  std::lock_guard<std::mutex> lock(runMutex);
+  return inferredUnits().members.at(unit);
+}
+
+double Invocation::timeUnit(size_t unit, uint64_t iterations) {
+  std::lock_guard<std::mutex> lock(runMutex);
+  return timeLaunch(inferredUnits().launches.at(unit), iterations);
+}
+
+std::vector<double> Invocation::profileUnits(uint64_t repeats) {
+  if (!repeats) throw std::invalid_argument("repeats must be positive");
+  std::lock_guard<std::mutex> lock(runMutex);
+  GraphExec &units = inferredUnits();
+  device->makeCurrent();
+  const size_t n = units.launches.size();
+  std::vector<std::vector<double>> prefix(n + 1);
+  hipEvent_t start = nullptr, stop = nullptr;
+  check(hipEventCreate(&start), "hipEventCreate");
+  try {
+    check(hipEventCreate(&stop), "hipEventCreate");
+    for (uint64_t r = 0; r < repeats; ++r)
+      for (size_t k = 0; k <= n; ++k) {
+        check(hipStreamSynchronize(stream), "hipStreamSynchronize");
+        check(hipEventRecord(start, stream), "hipEventRecord");
+        for (size_t u = 0; u < k; ++u) launchOne(units.launches[u], stream);
+        check(hipEventRecord(stop, stream), "hipEventRecord");
+        check(hipEventSynchronize(stop), "hipEventSynchronize");
+        float ms = 0;
+        check(hipEventElapsedTime(&ms, start, stop), "hipEventElapsedTime");
+        prefix[k].push_back(double(ms) * 1000.0);
+      }
+  } catch (...) {
+    hipEventDestroy(start);
+    if (stop) hipEventDestroy(stop);
+    throw;
+  }
+  hipEventDestroy(start);
+  hipEventDestroy(stop);
+  std::vector<double> medians(n + 1);
+  for (size_t k = 0; k <= n; ++k) {
+    std::sort(prefix[k].begin(), prefix[k].end());
+    medians[k] = prefix[k][prefix[k].size() / 2];
+  }
+  std::vector<double> out(n);
+  for (size_t k = 0; k < n; ++k) out[k] = medians[k + 1] - medians[k];
+  return out;
+}
+
+double Invocation::timeLaunch(const Launch &launch, uint64_t iterations) {
+  if (!iterations) throw std::invalid_argument("iterations must be positive");
   device->makeCurrent();
   check(hipStreamSynchronize(stream), "hipStreamSynchronize");
   hipEvent_t start = nullptr, stop = nullptr;

@@ -100,6 +100,7 @@ struct GraphExec {
   size_t nodeCount = 0;
   std::vector<std::vector<uint8_t>> storage;   // kernarg blocks referenced during capture
   std::vector<Launch> launches;                // the captured launch chain (grouped inferred policy)
+  std::vector<std::vector<size_t>> members;    // plan nodes each of those launches executes
   ~GraphExec();
 };
 
@@ -134,9 +135,23 @@ struct Invocation {
   // invocation stream, bracketed by HIP events.
   double timeNode(size_t index, uint64_t iterations);
   const std::string &nodeName(size_t index) const { return plan.nodes.at(index).launch.name; }
+  // The launches of one inferred (mode 1) step under the grouped policy: count, entry name, the
+  // plan nodes each executes, and the average duration of one launched `iterations` times.
+  size_t unitCount();
+  const std::string &unitName(size_t unit);
+  const std::vector<size_t> &unitMembers(size_t unit);
+  double timeUnit(size_t unit, uint64_t iterations);
+  // Per-launch durations of the inferred step in sequence (operands as cold as in a graph
+  // replay): prefixes of the step's launch chain (the first k launches, k = 0 .. count) are
+  // issued on the invocation stream between two HIP events, `repeats` times each; launch k's
+  // duration is the difference of the median times of prefixes k+1 and k, so the events' own
+  // cost cancels. The prefixes' effects are applied.
+  std::vector<double> profileUnits(uint64_t repeats);
 
 private:
   void validate(int mode, uint64_t batch) const;
+  GraphExec &inferredUnits();
+  double timeLaunch(const Launch &launch, uint64_t iterations);
   GraphExec &graphFor(int mode, uint64_t batch);
   void execute(int mode, uint64_t batch);
 };

@@ -78,6 +78,14 @@ _SIGNATURES = {
     "ckl_invocation_time_node": ([ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint64, ctypes.POINTER(ctypes.c_double)],
                                  ctypes.c_int),
     "ckl_invocation_node_name": ([ctypes.c_void_p, ctypes.c_uint64], ctypes.c_char_p),
+    "ckl_invocation_unit_count": ([ctypes.c_void_p, ctypes.POINTER(ctypes.c_uint64)], ctypes.c_int),
+    "ckl_invocation_unit_name": ([ctypes.c_void_p, ctypes.c_uint64, ctypes.POINTER(ctypes.c_char_p)], ctypes.c_int),
+    "ckl_invocation_unit_members": ([ctypes.c_void_p, ctypes.c_uint64, ctypes.POINTER(ctypes.c_uint64), ctypes.c_uint64,
+                                     ctypes.POINTER(ctypes.c_uint64)], ctypes.c_int),
+    "ckl_invocation_time_unit": ([ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint64, ctypes.POINTER(ctypes.c_double)],
+                                 ctypes.c_int),
+    "ckl_invocation_profile_units": ([ctypes.c_void_p, ctypes.c_uint64, ctypes.POINTER(ctypes.c_double), ctypes.c_uint64,
+                                      ctypes.POINTER(ctypes.c_uint64)], ctypes.c_int),
     "ckl_invocation_release": ([ctypes.c_void_p], None),
     "ckl_begin": ([ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint64], None),
     "ckl_module": ([ctypes.c_void_p, ctypes.c_char_p, ctypes.c_void_p, ctypes.c_uint64], None),

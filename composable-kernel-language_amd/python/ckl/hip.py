@@ -316,6 +316,43 @@ class Invocation(_ContextManager):
                                                                 ctypes.byref(out)))
         return out.value
 
+    def units(self) -> list:
+        """The launches of one inferred step (chains contracted, siblings grouped): a list of
+        (entry point, plan node indices)."""
+        lib = _native.native()
+        count = ctypes.c_uint64()
+        _native.check(lib.ckl_invocation_unit_count(self._native_resource.pointer, ctypes.byref(count)))
+        out = []
+        for unit in range(count.value):
+            name = ctypes.c_char_p()
+            _native.check(lib.ckl_invocation_unit_name(self._native_resource.pointer, unit, ctypes.byref(name)))
+            n = ctypes.c_uint64()
+            _native.check(lib.ckl_invocation_unit_members(self._native_resource.pointer, unit, None, 0, ctypes.byref(n)))
+            members = (ctypes.c_uint64 * max(1, n.value))()
+            _native.check(lib.ckl_invocation_unit_members(self._native_resource.pointer, unit, members, n.value,
+                                                          ctypes.byref(n)))
+            out.append((name.value.decode(), [int(members[k]) for k in range(n.value)]))
+        return out
+
+    def time_unit(self, unit: int, iterations: int = 20) -> float:
+        """Average microseconds of inferred-step launch `unit` issued `iterations` times back to back."""
+        out = ctypes.c_double()
+        _native.check(_native.native().ckl_invocation_time_unit(self._native_resource.pointer, unit, iterations,
+                                                                ctypes.byref(out)))
+        return out.value
+
+    def profile_units(self, repeats: int = 7) -> list:
+        """Durations (microseconds, `units()` order) of the inferred step's launches in sequence,
+        from the median times of the step's launch-chain prefixes (each issued `repeats` times
+        between HIP events; their effects are applied)."""
+        lib = _native.native()
+        count = ctypes.c_uint64()
+        _native.check(lib.ckl_invocation_unit_count(self._native_resource.pointer, ctypes.byref(count)))
+        out = (ctypes.c_double * max(1, count.value))()
+        _native.check(lib.ckl_invocation_profile_units(self._native_resource.pointer, repeats, out, count.value,
+                                                       ctypes.byref(count)))
+        return [float(out[k]) for k in range(count.value)]
+
     def benchmark(self, *, iterations=200, graph=False, mode=None, batch_size=1) -> dict:
         """Time `iterations` submissions of `batch_size` program executions with HIP events on
         the invocation stream; returns per-program stream and wall microseconds plus graph setup."""

@@ -261,9 +261,11 @@ def _rms_apply(shapes, consts, ext):
 # workspace. Measured on MI355X (B = 32): a B = 32 f32 GEMV costs 16 MFMA FLOP per weight byte,
 # so one CU's MFMA rate covers ~38 GB/s of weights and the matrix has to be spread over most of
 # the 256 CUs; but every cross-workgroup split adds a coherent write/read round trip, and one
-# front sweeping the weight rows in address order streams best. Hence: J = 4 (512 B of each
-# weight row per wave) once O alone yields >= 250 tiles, else J = 1, and a split only up to
-# ~256 workgroups with >= 512-row slices. The vector path (B <= 16, latency-bound) runs one
+# front sweeping the weight rows in address order streams best. The inferred graph hands the
+# split combine to the consuming chain kernel (csrc/runtime/chains.cpp), so splits there cost
+# only their partial planes. Measured inside the large decode step (weights not cached): J = 4
+# and no split for the LM head; J = 2 and 8 splits for the down projection (I > O); J = 1 and
+# 2 splits for gate/up (O > I); J = 1 and splits up to ~256 workgroups for square matrices. The vector path (B <= 16, latency-bound) runs one
 # workgroup per (64-column tile, batch row) whose up to 16 waves take 64 reduction rows each, all
 # loaded in one round trip; it splits only beyond 1024 rows.
 LINEAR_TARGET_GROUPS = 256
@@ -275,9 +277,16 @@ LINEAR_VECTOR_WAVE_ROWS = 64  # kVectorRows: reduction rows per wave
 
 def linear_tiling(b: int, i: int, o: int) -> dict:
     if b > LINEAR_VECTOR_ROWS and i % 4 == 0 and o % 4 == 0:
-        j = 4 if o >= 16384 else 1
+        if o >= 16384:                  # LM head: 512 B of each weight row per wave, no split
+            j, split = 4, 1
+        elif i > o:                     # down projection: long reductions, 64 columns per wave
+            j, split = 2, max(1, min(8, i // 512))
+        elif o > i:                     # gate/up projections
+            j, split = 1, max(1, min(2, i // 512))
+        else:
+            j = 1
+            split = max(1, min(LINEAR_TARGET_GROUPS // _cdiv(o, 32), i // 512))
         tiles = _cdiv(o, 32 * j)
-        split = max(1, min(LINEAR_TARGET_GROUPS // tiles, i // 512))
         chunk = _cdiv(_cdiv(i, split), 16) * 16
         split = _cdiv(i, chunk)
         rows, row_tiles = _cdiv(b, 32) * 32, _cdiv(b, 32)

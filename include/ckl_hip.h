@@ -144,6 +144,23 @@ int ckl_invocation_launch_count(ckl_invocation *invocation, int mode, uint64_t b
 int ckl_invocation_time_node(ckl_invocation *invocation, uint64_t index, uint64_t iterations, double *average_us);
 /* Device entry point name of plan node `index` ("" when out of range). */
 const char *ckl_invocation_node_name(ckl_invocation *invocation, uint64_t index);
+/* The launches one inferred step (mode 1, batch 1) submits after chain contraction and sibling
+ * grouping (no reference counterpart; measurement helpers like ckl_invocation_time_node):
+ * their number, entry point name (valid while the invocation lives), the plan nodes each one
+ * executes (up to `capacity` written to `members`, the total in *count), and the average
+ * duration of launch `unit` issued `iterations` times back to back on the invocation stream. */
+int ckl_invocation_unit_count(ckl_invocation *invocation, uint64_t *count);
+int ckl_invocation_unit_name(ckl_invocation *invocation, uint64_t unit, const char **name);
+int ckl_invocation_unit_members(ckl_invocation *invocation, uint64_t unit, uint64_t *members, uint64_t capacity,
+                                uint64_t *count);
+int ckl_invocation_time_unit(ckl_invocation *invocation, uint64_t unit, uint64_t iterations, double *average_us);
+/* Durations of the inferred step's launches in sequence (operands as cold as in a graph replay):
+ * every prefix of the launch chain (its first k launches, k = 0 .. count) is issued `repeats`
+ * times between two HIP events, and launch k's duration is the difference of the median times
+ * of prefixes k+1 and k (the events' cost cancels). The prefixes' effects are applied. Writes up
+ * to `capacity` durations in microseconds; the launch count in *count. */
+int ckl_invocation_profile_units(ckl_invocation *invocation, uint64_t repeats, double *durations_us, uint64_t capacity,
+                                 uint64_t *count);
 void ckl_invocation_release(ckl_invocation *invocation);
 
 /* ---------------------------------------------------------------- host-entry callbacks
