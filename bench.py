@@ -194,9 +194,8 @@ def kernel_roofline(session, c, samples=7):
     replay: launch k's duration is the difference of the median HIP-event times of the step's
     first k+1 and first k launches (`samples` repeats each). Returns per-family totals and the roofline entry of the dominant family
     (largest total time per step): algorithmic bytes per launch / average launch duration. A
-    launch's algorithmic bytes are the sum of its plan nodes' (exact for plain and grouped linear
-    launches; for chains this also counts hand-offs kept on chip, a few per cent at most of the
-    attention chain's bytes)."""
+    launch's algorithmic bytes are the sum of its plan nodes' less the hand-offs a chain keeps on
+    chip (the attention chain's scores and probabilities, silu's output, the rotated k)."""
     inv = session.invocations[True]
     position = c.context - 1
     nodes = decoder_node_bytes(c, position)
@@ -206,6 +205,12 @@ def kernel_roofline(session, c, samples=7):
     session.state.reset(LIGHT_RESET)
     durations = inv.profile_units(samples)
     session.state.reset()
+    b, h, f, a, rows = c.batch, c.hidden, c.ffn, c.heads, position + 1
+    # Hand-offs a chain keeps on chip (written by one member, read by the next): not HBM traffic.
+    on_chip = {"attention_scores__softmax__attention_values": 16 * b * a * rows,   # scores, probs
+               "softmax__attention_values": 8 * b * a * rows,                     # probs
+               "silu__multiply": 8 * b * f,                                        # activation
+               "rope__rope__append_kv": 8 * b * h}                                 # rotated k
     per_kernel = {}
     for index, (name, members) in enumerate(units):
         families = {nodes[m][0] for m in members}
@@ -219,7 +224,7 @@ def kernel_roofline(session, c, samples=7):
         entry["launches"] += 1
         entry["nodes"] += len(members)
         entry["total_us"] += us
-        entry["bytes"] += sum(nodes[m][1] for m in members)
+        entry["bytes"] += sum(nodes[m][1] for m in members) - on_chip.get(family, 0)
         entry["entries"].add(name)
     session.state.reset()
     summary = {k: {"launches": v["launches"], "plan_nodes": v["nodes"], "avg_us": v["total_us"] / v["launches"],
@@ -318,6 +323,8 @@ def main():
         for family, row in summary.items():
             log(f"[{name}] {family:38s} launches={row['launches']:3d} avg={row['avg_us']:9.2f} us "
                 f"total={row['total_us']:9.2f} us  {row['achieved_GBps']:8.1f} GB/s")
+        result["kernel_families"] = {k: {"launches": v["launches"], "avg_us": v["avg_us"], "achieved_GBps": v["achieved_GBps"],
+                                         "frac": v["achieved_GBps"] * 1e9 / HBM_PEAK} for k, v in summary.items()}
         if name == "large":
             result["roofline"] = roofline
             log(f"[large] dominant kernel {dominant}: {roofline}")

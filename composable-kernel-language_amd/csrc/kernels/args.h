@@ -92,6 +92,7 @@ struct CKL_ALIGN SiluMultiplyChainArgs { UnaryArgs silu; BinaryArgs multiply; Pa
 struct CKL_ALIGN SoftmaxValuesChainArgs { SoftmaxArgs softmax; ValuesArgs values; };
 struct CKL_ALIGN AttentionChainArgs { ScoresArgs scores; SoftmaxArgs softmax; ValuesArgs values; };
 struct CKL_ALIGN RopeAppendChainArgs { RopeArgs q; RopeArgs k; AppendArgs append; PartialSource qsrc, ksrc, v; };
+struct CKL_ALIGN GreedyAdvanceChainArgs { GreedyArgs greedy; AdvanceArgs advance; };
 
 // Largest row (in floats) an attention chain keeps in LDS.
 constexpr int kChainSoftmaxRow = 8192;

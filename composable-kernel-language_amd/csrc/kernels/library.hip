@@ -362,20 +362,19 @@ __device__ __forceinline__ float partial_load(const float *p) {
   return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Returns true in every thread of the last workgroup to finish a split tile. Only wave 0 of a
-// workgroup writes its partial tile; it waits until those agent-coherent stores have completed
-// (s_waitcnt vmcnt(0)) before bumping the tile's completion counter, so the workgroup that
+// Returns true in every thread of the last workgroup to finish a split tile. Every wave waits
+// until its agent-coherent partial stores have completed (s_waitcnt vmcnt(0)); after the
+// workgroup barrier one thread bumps the tile's completion counter, so the workgroup that
 // observes the final count reads every partial through the same coherent path.
-__device__ __forceinline__ bool split_arrive(unsigned *counter, int parts, int wave) {
+__device__ __forceinline__ bool split_arrive(unsigned *counter, int parts) {
   __shared__ int last;
-  if (wave == 0) {
-    __builtin_amdgcn_s_waitcnt(kWaitStores);
-    if (threadIdx.x == 0) {
-      unsigned previous = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      int isLast = previous == unsigned(parts - 1);
-      if (isLast) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      last = isLast;
-    }
+  __builtin_amdgcn_s_waitcnt(kWaitStores);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned previous = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    int isLast = previous == unsigned(parts - 1);
+    if (isLast) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last = isLast;
   }
   __syncthreads();
   return last;
@@ -588,43 +587,52 @@ template <MfmaFlavour F, int J, int S> __device__ void linear_mfma(const LinearA
     stage_compute<F, J, 1>(st, acc);
   }
 
-  // Waves 1..3 hand their tiles to wave 0 through LDS; wave 0 adds them in wave order.
-  if (wave > 0) {
-#pragma unroll
-    for (int j = 0; j < J; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) smem[(((wave - 1) * J + j) * 16 + r) * 64 + lane] = acc[j][r];
-  }
-  __syncthreads();
+  // Every wave hands its tile to the others through LDS; wave w then adds rows {8w + 4s + q} of
+  // the tile (its accumulator registers 4w .. 4w+3) in wave order and stores them, so the four
+  // waves share the epilogue. Columns go through LDS in groups of JH (at most 2: 32 KB).
+  // Partial planes the consumer combines (deferred) are plain stores; planes combined here go
+  // through the agent-coherent path.
+  constexpr int JH = J < 2 ? J : 2;
   const int rowTiles = (a.B + 31) / 32;
   float *partial = split_partials(a, false);
-  if (wave == 0) {
-#pragma unroll 1
-    for (int v = 1; v < 4; ++v)
 #pragma unroll
-      for (int j = 0; j < J; ++j)
+  for (int h = 0; h < J; h += JH) {
+    if (h > 0) __syncthreads();
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[j][r] += smem[(((v - 1) * J + j) * 16 + r) * 64 + lane];
-    // D[i][c] of MFMA j: i = 8*(r/4) + 4*s + r%4, c = lane%32 -> column n + j.
+    for (int j = 0; j < JH; ++j)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int i = rt * 32 + 8 * (r / 4) + 4 * s + (r % 4);
+      for (int r = 0; r < 16; ++r) smem[((wave * JH + j) * 16 + r) * 64 + lane] = acc[h + j][r];
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      float sum[JH];
+#pragma unroll
+      for (int j = 0; j < JH; ++j) sum[j] = smem[(j * 16 + 4 * wave + q) * 64 + lane];
+#pragma unroll
+      for (int v = 1; v < 4; ++v)
+#pragma unroll
+        for (int j = 0; j < JH; ++j) sum[j] += smem[((v * JH + j) * 16 + 4 * wave + q) * 64 + lane];
+      const int i = rt * 32 + 8 * wave + 4 * s + q;   // row of accumulator register 4*wave + q
       if (!colOk) continue;
       if (a.kSplit > 1) {
-        float *p = partial + long(kg) * rowTiles * 32 * a.O + long(i) * a.O + n;
+        float *p = partial + long(kg) * rowTiles * 32 * a.O + long(i) * a.O + n + h;
+        if (a.deferred) {
+          if constexpr (JH == 2) *reinterpret_cast<float2 *>(p) = make_float2(sum[0], sum[1]);
+          else *p = sum[0];
+        } else {
 #pragma unroll
-        for (int j = 0; j < J; ++j) partial_store(p + j, acc[j][r]);
+          for (int j = 0; j < JH; ++j) partial_store(p + j, sum[j]);
+        }
       } else if (i < a.B) {
-        float *p = a.dst + long(i) * a.O + n;
-        if constexpr (J == 4) *reinterpret_cast<float4 *>(p) = make_float4(acc[0][r], acc[1][r], acc[2][r], acc[3][r]);
-        else if constexpr (J == 2) *reinterpret_cast<float2 *>(p) = make_float2(acc[0][r], acc[1][r]);
-        else *p = acc[0][r];
+        float *p = a.dst + long(i) * a.O + n + h;
+        if constexpr (JH == 2) *reinterpret_cast<float2 *>(p) = make_float2(sum[0], sum[1]);
+        else *p = sum[0];
       }
     }
   }
   if (a.kSplit > 1 && !a.deferred) {
     unsigned *counters = split_counters(a);
-    if (split_arrive(counters + rt * a.tilesN + tn, a.kSplit, wave))
+    if (split_arrive(counters + rt * a.tilesN + tn, a.kSplit))
       split_finish(a, partial, long(rowTiles) * 32 * a.O, rt * 32, 32, tn * 32 * J, 32 * J);
   }
 }
@@ -679,7 +687,7 @@ __device__ void linear_rowvec_body(const LinearArgs &a, int block) {
     if (a.kSplit > 1) partial_store(split_partials(a, true) + (long(kg) * a.B + b) * a.O + col, v);
     else a.dst[long(b) * a.O + col] = v;
   }
-  if (a.kSplit > 1 && !a.deferred && split_arrive(split_counters(a) + b * a.tilesN + tn, a.kSplit, wave))
+  if (a.kSplit > 1 && !a.deferred && split_arrive(split_counters(a) + b * a.tilesN + tn, a.kSplit))
     split_finish(a, split_partials(a, true), long(a.B) * a.O, b, 1, tn * 64, 64);
 }
 
@@ -1129,7 +1137,8 @@ CKL_ENTRY(silu__multiply, SiluMultiplyChainArgs, silu__multiply_body)
 // otherwise it folds the pair into the row's 64-bit key (ordered value bits << 32 | ~index, so
 // the maximum key is the largest value at the smallest index) with an agent-scope atomic max
 // and bumps the row's counter; the last workgroup writes the token and resets key and counter.
-// workspace: uint64 key[B], then uint32 counter[B].
+// workspace: uint64 key[B], uint32 counter[B], then the uint32 row count of the greedy ->
+// advance chain.
 constexpr int kGreedyChunk = 4096;
 
 __device__ __forceinline__ unsigned long long greedy_key(float v, int index) {
@@ -1138,10 +1147,12 @@ __device__ __forceinline__ unsigned long long greedy_key(float v, int index) {
   return (static_cast<unsigned long long>(ordered) << 32) | (0xFFFFFFFFu - unsigned(index));
 }
 
-__device__ void greedy_body(const GreedyArgs &a, int block) {
+// Returns true in thread 0 of the workgroup that wrote row b's token; *position is the position
+// it read.
+__device__ __forceinline__ bool greedy_block(const GreedyArgs &a, int block, int *position) {
   __shared__ unsigned long long bestKey[kBlock / 64];
   const int b = block / a.chunks, chunk = block % a.chunks;
-  if (b >= a.B) return;
+  if (b >= a.B) return false;
   const float *logits = a.logits + long(b) * a.V;
   const int v0 = chunk * kGreedyChunk, v1 = min(v0 + kGreedyChunk, a.V);
   unsigned long long key = 0;                               // below every real key
@@ -1161,7 +1172,7 @@ __device__ void greedy_body(const GreedyArgs &a, int block) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   if (lane == 0) bestKey[wave] = key;
   __syncthreads();
-  if (threadIdx.x != 0) return;
+  if (threadIdx.x != 0) return false;
   for (int w = 1; w < kBlock / 64; ++w) key = max(key, bestKey[w]);
   bool finish = a.chunks == 1;
   if (!finish) {
@@ -1177,14 +1188,37 @@ __device__ void greedy_body(const GreedyArgs &a, int block) {
       __hip_atomic_store(counters + b, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
-  if (!finish) return;
+  if (!finish) return false;
   float first = logits[0];
   int winner = (first != first || key == 0) ? 0 : int(0xFFFFFFFFu - unsigned(key & 0xFFFFFFFFu));
   int p = load_position(a.position);
   a.tokens[b] = winner;
   if (p >= 0 && p < a.T) a.history[long(p) * a.B + b] = winner;
+  *position = p;
+  return true;
+}
+__device__ void greedy_body(const GreedyArgs &a, int block) {
+  int p;
+  greedy_block(a, block, &p);
 }
 CKL_ENTRY(greedy, GreedyArgs, greedy_body)
+
+// greedy -> advance as one launch of greedy's geometry: the thread that writes a row's token
+// waits for its position load and stores to complete, then counts the row; the one that counts
+// the last row (every row has read the position by then) resets the count and stores
+// position + 1, which is what advance computes.
+__device__ void greedy__advance_body(const GreedyAdvanceChainArgs &a, int block) {
+  int p;
+  if (!greedy_block(a.greedy, block, &p)) return;
+  __builtin_amdgcn_s_waitcnt(kWaitStores);
+  unsigned *rows = reinterpret_cast<unsigned *>(a.greedy.workspace + 12 * a.greedy.B);
+  unsigned previous = __hip_atomic_fetch_add(rows, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (previous == unsigned(a.greedy.B - 1)) {
+    __hip_atomic_store(rows, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    a.advance.position[0] = p + 1;
+  }
+}
+CKL_ENTRY(greedy__advance, GreedyAdvanceChainArgs, greedy__advance_body)
 
 // ------------------------------------------------------------------ advance
 // position[0] += 1   (workloads.py:186-188)

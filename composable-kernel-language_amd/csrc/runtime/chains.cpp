@@ -5,7 +5,7 @@
 // entry points (csrc/kernels/library.hip) that run several dependent dispatches row by row in one
 // grid: rms_stats -> rms_apply, add -> rms_stats -> rms_apply, embedding -> rms_stats ->
 // rms_apply, silu -> multiply, attention_scores -> softmax -> attention_values (or softmax ->
-// attention_values) and rope(q), rope(k) -> append_kv. The plan itself (nodes, edges,
+// attention_values), rope(q), rope(k) -> append_kv and greedy -> advance. The plan itself (nodes, edges,
 // argument blocks) is unchanged; only the inferred lowering contracts a chain into one unit.
 //
 // A chain is taken only when
@@ -272,6 +272,24 @@ const char *ropeAppendChain(const Members &m, const Internal &internal, Launch &
   return nullptr;
 }
 
+const char *greedyAdvanceChain(const Members &m, const Internal &, Launch &out) {
+  GreedyAdvanceChainArgs c{block<GreedyArgs>(*m[0]), block<AdvanceArgs>(*m[1])};
+  const GreedyArgs &g = c.greedy;
+  if (c.advance.position != g.position || !g.workspace || g.B <= 0 || g.V <= 0 || g.T <= 0 || g.chunks <= 0)
+    return "advance does not step greedy's position";
+  // The position is read by every row and written once after all reads (the chain's row count);
+  // it must not overlap the other buffers.
+  std::vector<Range> ranges{whole(g.logits, 4ull * uint64_t(g.B) * uint64_t(g.V)), rows(g.tokens, uint64_t(g.B), 4, true),
+                            slab(g.history, 4ull * uint64_t(g.T) * uint64_t(g.B), true), slab(g.position, 4, true)};
+  if (!hazardFree(ranges)) return kOverlap;
+  const Launch &greedy = *m[0];
+  out.grid[0] = greedy.grid[0];
+  out.block[0] = greedy.block[0];
+  out.shared = greedy.shared;
+  setArguments(out, c);
+  return nullptr;
+}
+
 using Successors = std::vector<std::vector<size_t>>;
 using Matcher = std::vector<size_t> (*)(const Plan &, size_t head, const Successors &, const std::vector<bool> &taken);
 
@@ -329,6 +347,7 @@ const std::vector<Rule> &rules() {
       {{"ckl_attention_scores", "ckl_softmax", "ckl_attention_values"}, "ckl_attention_scores__softmax__attention_values",
        attentionChain},
       {{"ckl_softmax", "ckl_attention_values"}, "ckl_softmax__attention_values", softmaxValuesChain},
+      {{"ckl_greedy", "ckl_advance"}, "ckl_greedy__advance", greedyAdvanceChain},
       {{"ckl_rope", "ckl_rope", "ckl_append_kv"}, "ckl_rope__rope__append_kv", ropeAppendChain, matchRopeAppend,
        {{0, offsetof(RopeArgs, src), offsetof(RopeAppendChainArgs, qsrc)},
         {1, offsetof(RopeArgs, src), offsetof(RopeAppendChainArgs, ksrc)},

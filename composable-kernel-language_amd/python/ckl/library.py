@@ -263,9 +263,10 @@ def _rms_apply(shapes, consts, ext):
 # the 256 CUs; but every cross-workgroup split adds a coherent write/read round trip, and one
 # front sweeping the weight rows in address order streams best. The inferred graph hands the
 # split combine to the consuming chain kernel (csrc/runtime/chains.cpp), so splits there cost
-# only their partial planes. Measured inside the large decode step (weights not cached): J = 4
-# and no split for the LM head; J = 2 and 8 splits for the down projection (I > O); J = 1 and
-# 2 splits for gate/up (O > I); J = 1 and splits up to ~256 workgroups for square matrices. The vector path (B <= 16, latency-bound) runs one
+# only their partial planes. Measured inside the large decode step (weights not cached; a cold
+# streaming probe of these shapes needs >= ~700 workgroups in flight to pass 4.5 TB/s): J = 4
+# and no split for the LM head; J = 2 with 8 slices for square and down projections (I >= O)
+# and 4 slices for gate/up (O > I), slices of at least 256 rows. The vector path (B <= 16, latency-bound) runs one
 # workgroup per (64-column tile, batch row) whose up to 16 waves take 64 reduction rows each, all
 # loaded in one round trip; it splits only beyond 1024 rows.
 LINEAR_TARGET_GROUPS = 256
@@ -279,18 +280,13 @@ def linear_tiling(b: int, i: int, o: int) -> dict:
     if b > LINEAR_VECTOR_ROWS and i % 4 == 0 and o % 4 == 0:
         if o >= 16384:                  # LM head: 512 B of each weight row per wave, no split
             j, split = 4, 1
-        elif i > o:                     # down projection: long reductions, 64 columns per wave
-            j, split = 2, max(1, min(8, i // 512))
-        elif o > i:                     # gate/up projections
-            j, split = 1, max(1, min(2, i // 512))
-        else:
-            j = 1
-            split = max(1, min(LINEAR_TARGET_GROUPS // _cdiv(o, 32), i // 512))
+        else:                           # 64 columns per wave; 8 slices (I >= O) or 4 (gate/up)
+            j, split = 2, max(1, min(8 if i >= o else 4, i // 256))
         tiles = _cdiv(o, 32 * j)
         chunk = _cdiv(_cdiv(i, split), 16) * 16
         split = _cdiv(i, chunk)
         rows, row_tiles = _cdiv(b, 32) * 32, _cdiv(b, 32)
-        shared = 3 * j * 16 * 64 * 4
+        shared = 4 * min(j, 2) * 16 * 64 * 4          # the 4 waves' accumulator tiles, 2 columns at a time
         stage = 1
         entry = f"ckl_linear_mfma{j}x{stage}"
         block = BLOCK
@@ -388,7 +384,7 @@ def _greedy(shapes, consts, ext):
     if not (ext[0] >= b and ext[1:] == (1, 1)):
         return None
     chunks = _cdiv(v, GREEDY_CHUNK)
-    workspace = 256 if chunks == 1 else _cdiv(12 * b, 256) * 256
+    workspace = _cdiv(12 * b + 4, 256) * 256       # keys, counters, row count (greedy -> advance chain)
     return Launch(b * chunks, (b, v, t, chunks), workspace=workspace)
 
 

@@ -1,6 +1,6 @@
 """Library chains in the inferred graph (csrc/runtime/chains.cpp): contracted launches leave exactly
 the state the ordinary launches leave, bit for bit, the decode step runs in 9 launches per layer
-plus 4, and a chain whose buffers overlap in a way row-by-row execution would change runs unfused."""
+plus 3, and a chain whose buffers overlap in a way row-by-row execution would change runs unfused."""
 import numpy as np
 import pytest
 
@@ -24,8 +24,8 @@ SPLIT_VECTOR = Config(batch=5, hidden=1280, heads=10, layers=1, ffn=1536, vocab=
 
 def chained_launches(layers):
     # embedding+rms; per layer: QKV, rope pair+append, scores+softmax+values, O, add+rms,
-    # gate/up, silu+multiply, down, add+rms; then lm head, greedy, advance.
-    return 1 + 9 * layers + 3
+    # gate/up, silu+multiply, down, add+rms; then lm head, greedy+advance.
+    return 1 + 9 * layers + 2
 
 
 @pytest.mark.parametrize("config", [CONFIGS["small"], REFERENCE_SMALL, AWKWARD, ODD, SPLIT_MFMA, SPLIT_VECTOR],
