@@ -195,7 +195,7 @@ def kernel_roofline(session, c, samples=7):
     first k+1 and first k launches (`samples` repeats each). Returns per-family totals and the roofline entry of the dominant family
     (largest total time per step): algorithmic bytes per launch / average launch duration. A
     launch's algorithmic bytes are the sum of its plan nodes' less the hand-offs a chain keeps on
-    chip (the attention chain's scores and probabilities, silu's output, the rotated k)."""
+    chip (the attention chain's scores and probabilities, silu's output, the rotated q and k)."""
     inv = session.invocations[True]
     position = c.context - 1
     nodes = decoder_node_bytes(c, position)
@@ -210,7 +210,9 @@ def kernel_roofline(session, c, samples=7):
     on_chip = {"attention_scores__softmax__attention_values": 16 * b * a * rows,   # scores, probs
                "softmax__attention_values": 8 * b * a * rows,                     # probs
                "silu__multiply": 8 * b * f,                                        # activation
-               "rope__rope__append_kv": 8 * b * h}                                 # rotated k
+               "rope__rope__append_kv": 8 * b * h,                                 # rotated k
+               # rotated k, the attention's read of the rotated q, scores, probs
+               "rope__rope__append_kv__attention_scores__softmax__attention_values": 12 * b * h + 16 * b * a * rows}
     per_kernel = {}
     for index, (name, members) in enumerate(units):
         families = {nodes[m][0] for m in members}

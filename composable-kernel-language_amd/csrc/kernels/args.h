@@ -93,6 +93,11 @@ struct CKL_ALIGN SoftmaxValuesChainArgs { SoftmaxArgs softmax; ValuesArgs values
 struct CKL_ALIGN AttentionChainArgs { ScoresArgs scores; SoftmaxArgs softmax; ValuesArgs values; };
 struct CKL_ALIGN RopeAppendChainArgs { RopeArgs q; RopeArgs k; AppendArgs append; PartialSource qsrc, ksrc, v; };
 struct CKL_ALIGN GreedyAdvanceChainArgs { GreedyArgs greedy; AdvanceArgs advance; };
+// rope(q), rope(k) -> append_kv -> attention_scores -> softmax -> attention_values per (b, h).
+struct CKL_ALIGN RopeAttentionChainArgs {
+  RopeArgs q; RopeArgs k; AppendArgs append; ScoresArgs scores; SoftmaxArgs softmax; ValuesArgs values;
+  PartialSource qsrc, ksrc, v;
+};
 
 // Largest row (in floats) an attention chain keeps in LDS.
 constexpr int kChainSoftmaxRow = 8192;

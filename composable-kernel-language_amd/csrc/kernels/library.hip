@@ -32,6 +32,7 @@ constexpr int kBlock = 256;
 #define CKL_ENTRY(name, Args, body) CKL_ENTRY_ATTR(name, Args, body, kBlock, )
 // Streaming kernels that keep several loads in flight per lane trade occupancy for registers.
 #define CKL_TWO_WAVES __attribute__((amdgpu_waves_per_eu(1, 2)))
+#define CKL_ONE_WAVE __attribute__((amdgpu_waves_per_eu(1, 1)))
 
 // ------------------------------------------------------------------ wave64 reductions (DPP)
 template <int Ctrl> __device__ __forceinline__ float dpp(float v) {
@@ -97,32 +98,51 @@ __device__ __forceinline__ int load_position(const int *position) { return *posi
 // Operands of chain kernels that may be a split linear's partial planes (PartialSource, args.h):
 // the planes are added in g order starting from 0, as the linear's own combine (split_finish)
 // does, so deferring the combine leaves every value bit-identical. `i` is the element index.
-__device__ __forceinline__ float source1(const PartialSource &src, const float *own, long i) {
-  if (src.parts == 0) return own[i];
-  float t = 0.f;
-#pragma unroll 4
-  for (int g = 0; g < src.parts; ++g) t += src.partials[g * src.planeStride + i];
+// The planes of a batch are loaded together (one round trip per kSourceBatch planes): indices
+// past the last plane re-read it and add nothing (the running sum starts at +0 and is never -0,
+// so skipping a term and adding +0 agree).
+constexpr int kSourceBatch = 8;
+template <int N> struct SourceVector { float v[N]; };
+template <int N> __device__ __forceinline__ SourceVector<N> source_load(const float *p) {
+  SourceVector<N> out;
+  if constexpr (N == 4) {
+    float4 v = *reinterpret_cast<const float4 *>(p);
+    out.v[0] = v.x; out.v[1] = v.y; out.v[2] = v.z; out.v[3] = v.w;
+  } else if constexpr (N == 2) {
+    float2 v = *reinterpret_cast<const float2 *>(p);
+    out.v[0] = v.x; out.v[1] = v.y;
+  } else {
+    out.v[0] = *p;
+  }
+  return out;
+}
+template <int N> __device__ __forceinline__ SourceVector<N> source(const PartialSource &src, const float *own, long i) {
+  if (src.parts == 0) return source_load<N>(own + i);
+  SourceVector<N> t;
+#pragma unroll
+  for (int e = 0; e < N; ++e) t.v[e] = 0.f;
+  for (int g0 = 0; g0 < src.parts; g0 += kSourceBatch) {
+    SourceVector<N> v[kSourceBatch];
+#pragma unroll
+    for (int j = 0; j < kSourceBatch; ++j)
+      v[j] = source_load<N>(src.partials + long(min(g0 + j, src.parts - 1)) * src.planeStride + i);
+#pragma unroll
+    for (int j = 0; j < kSourceBatch; ++j)
+#pragma unroll
+      for (int e = 0; e < N; ++e) t.v[e] += g0 + j < src.parts ? v[j].v[e] : 0.f;
+  }
   return t;
+}
+__device__ __forceinline__ float source1(const PartialSource &src, const float *own, long i) {
+  return source<1>(src, own, i).v[0];
 }
 __device__ __forceinline__ float2 source2(const PartialSource &src, const float *own, long i) {
-  if (src.parts == 0) return *reinterpret_cast<const float2 *>(own + i);
-  float2 t = make_float2(0.f, 0.f);
-#pragma unroll 4
-  for (int g = 0; g < src.parts; ++g) {
-    float2 v = *reinterpret_cast<const float2 *>(src.partials + g * src.planeStride + i);
-    t.x += v.x; t.y += v.y;
-  }
-  return t;
+  SourceVector<2> t = source<2>(src, own, i);
+  return make_float2(t.v[0], t.v[1]);
 }
 __device__ __forceinline__ float4 source4(const PartialSource &src, const float *own, long i) {
-  if (src.parts == 0) return *reinterpret_cast<const float4 *>(own + i);
-  float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll 4
-  for (int g = 0; g < src.parts; ++g) {
-    float4 v = *reinterpret_cast<const float4 *>(src.partials + g * src.planeStride + i);
-    t.x += v.x; t.y += v.y; t.z += v.z; t.w += v.w;
-  }
-  return t;
+  SourceVector<4> t = source<4>(src, own, i);
+  return make_float4(t.v[0], t.v[1], t.v[2], t.v[3]);
 }
 
 // ------------------------------------------------------------------ embedding
@@ -421,13 +441,16 @@ template <int J> __device__ __forceinline__ void load_columns(float (&out)[J], c
 // clamped to 0) only feeds output row >= B and a column >= O (clamped to column 0) only feeds
 // output column >= O, neither of which is stored. Tail stages (S = 1) zero reduction rows past k1
 // (their addresses are clamped to row k1-1).
-template <int J, int S> struct MfmaStage {
+// M > 1: M weight matrices of one shape that multiply the same x (a shared-operand group); the
+// stage holds one x fragment and each member's weight columns.
+template <int J, int S, int M> struct MfmaStage {
   float x[2 * S][4];
-  float w[2 * S][4][J];
+  float w[M][2 * S][4][J];
 };
 
-template <int J, int S, bool Tail>
-__device__ __forceinline__ void mfma_load(MfmaStage<J, S> &st, const float *xr, const float *w, long O, int k, int k1) {
+template <int J, int S, int M, bool Tail>
+__device__ __forceinline__ void mfma_load(MfmaStage<J, S, M> &st, const float *xr, const float *const (&w)[M], long O,
+                                          int k, int k1) {
 #pragma unroll
   for (int u = 0; u < 2 * S; ++u) {
     const int kk = k + 8 * u;
@@ -441,24 +464,34 @@ __device__ __forceinline__ void mfma_load(MfmaStage<J, S> &st, const float *xr, 
         const bool inside = kk + i < k1;
         const int kr = min(kk + i, k1 - 1);
         st.x[u][i] = inside ? xr[kr] : 0.f;
-        float c[J];
-        load_columns<J>(c, w + long(kr) * O);
 #pragma unroll
-        for (int j = 0; j < J; ++j) st.w[u][i][j] = inside ? c[j] : 0.f;
+        for (int m = 0; m < M; ++m) {
+          float c[J];
+          load_columns<J>(c, w[m] + long(kr) * O);
+#pragma unroll
+          for (int j = 0; j < J; ++j) st.w[m][u][i][j] = inside ? c[j] : 0.f;
+        }
       } else {
-        load_columns<J>(st.w[u][i], w + long(kk + i) * O);
+#pragma unroll
+        for (int m = 0; m < M; ++m) load_columns<J>(st.w[m][u][i], w[m] + long(kk + i) * O);
       }
     }
   }
 }
 
-template <int J, int S> __device__ __forceinline__ void mfma_compute(const MfmaStage<J, S> &st, floatx16 (&acc)[J]) {
+// Each accumulator acc[m][j] sees the same sequence of products whatever M is, so a member of a
+// shared-operand group computes exactly what it computes alone.
+template <int J, int S, int M>
+__device__ __forceinline__ void mfma_compute(const MfmaStage<J, S, M> &st, floatx16 (&acc)[M][J]) {
 #pragma unroll
   for (int u = 0; u < 2 * S; ++u)
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < J; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(st.x[u][i], st.w[u][i][j], acc[j], 0, 0, 0);
+      for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int j = 0; j < J; ++j)
+          acc[m][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(st.x[u][i], st.w[m][u][i][j], acc[m][j], 0, 0, 0);
 }
 
 // Split-bf16 flavour: v_mfma_f32_32x32x16_bf16 at 16x the f32 MFMA rate. Every f32 operand is split
@@ -498,7 +531,8 @@ __device__ __forceinline__ bf16x8 as_bf16x8(const unsigned (&p)[4]) {
   return __builtin_bit_cast(bf16x8, make_uint4(p[0], p[1], p[2], p[3]));
 }
 
-template <int J, int S> __device__ __forceinline__ void mfma_compute_bf16(const MfmaStage<J, S> &st, floatx16 (&acc)[J]) {
+template <int J, int S, int M>
+__device__ __forceinline__ void mfma_compute_bf16(const MfmaStage<J, S, M> &st, floatx16 (&acc)[M][J]) {
 #pragma unroll
   for (int t = 0; t < S; ++t) {
     float xv[8];
@@ -508,48 +542,60 @@ template <int J, int S> __device__ __forceinline__ void mfma_compute_bf16(const 
     split_bf16(xv, xs);
     const bf16x8 xh = as_bf16x8(xs.hi), xm = as_bf16x8(xs.mid), xl = as_bf16x8(xs.lo);
 #pragma unroll
-    for (int j = 0; j < J; ++j) {
-      float wv[8];
+    for (int m = 0; m < M; ++m)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) { wv[i] = st.w[2 * t][i][j]; wv[4 + i] = st.w[2 * t + 1][i][j]; }
-      SplitBf16 ws;
-      split_bf16(wv, ws);
-      const bf16x8 wh = as_bf16x8(ws.hi), wm = as_bf16x8(ws.mid), wl = as_bf16x8(ws.lo);
-      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xm, wm, acc[j], 0, 0, 0);
-      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xl, wh, acc[j], 0, 0, 0);
-      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh, wl, acc[j], 0, 0, 0);
-      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xm, wh, acc[j], 0, 0, 0);
-      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh, wm, acc[j], 0, 0, 0);
-      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh, wh, acc[j], 0, 0, 0);
-    }
+      for (int j = 0; j < J; ++j) {
+        float wv[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) { wv[i] = st.w[m][2 * t][i][j]; wv[4 + i] = st.w[m][2 * t + 1][i][j]; }
+        SplitBf16 ws;
+        split_bf16(wv, ws);
+        const bf16x8 wh = as_bf16x8(ws.hi), wm = as_bf16x8(ws.mid), wl = as_bf16x8(ws.lo);
+        floatx16 &c = acc[m][j];
+        c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xm, wm, c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xl, wh, c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh, wl, c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xm, wh, c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh, wm, c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh, wh, c, 0, 0, 0);
+      }
   }
 }
 
 enum class MfmaFlavour { F32, SplitBf16 };
-template <MfmaFlavour F, int J, int S> __device__ __forceinline__ void stage_compute(const MfmaStage<J, S> &st, floatx16 (&acc)[J]) {
-  if constexpr (F == MfmaFlavour::F32) mfma_compute<J, S>(st, acc);
-  else mfma_compute_bf16<J, S>(st, acc);
+template <MfmaFlavour F, int J, int S, int M>
+__device__ __forceinline__ void stage_compute(const MfmaStage<J, S, M> &st, floatx16 (&acc)[M][J]) {
+  if constexpr (F == MfmaFlavour::F32) mfma_compute<J, S, M>(st, acc);
+  else mfma_compute_bf16<J, S, M>(st, acc);
 }
 
-template <MfmaFlavour F, int J, int S> __device__ void linear_mfma(const LinearArgs &a, int block, float *smem) {
+// `a` holds M member blocks that agree on x, B, I, O, layer and the tiling (M = 1: one linear);
+// the workgroup computes its tile of every member from one stream of x fragments.
+template <MfmaFlavour F, int J, int S, int M>
+__device__ void linear_mfma(const LinearArgs *a, int block, float *smem) {
+  const LinearArgs &a0 = a[0];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform: scalar loop control
   const int m = lane & 31, s = lane >> 5;
-  const int tn = block % a.tilesN, rest = block / a.tilesN;
-  const int kg = rest % a.kSplit, rt = rest / a.kSplit;
+  const int tn = block % a0.tilesN, rest = block / a0.tilesN;
+  const int kg = rest % a0.kSplit, rt = rest / a0.kSplit;
   const int n = tn * 32 * J + J * m;               // first of this lane's J columns
-  const bool colOk = n < a.O;                      // host guarantees O % J == 0
+  const bool colOk = n < a0.O;                     // host guarantees O % J == 0
   const int row = rt * 32 + m;
-  const bool rowOk = row < a.B;
-  const float *xr = a.x + long(rowOk ? row : 0) * a.I;
-  const float *w = a.w + long(a.layer) * a.I * a.O + (colOk ? n : 0);
-  const int kb0 = min(kg * a.kChunk, a.I), kb1 = min(kb0 + a.kChunk, a.I);
+  const bool rowOk = row < a0.B;
+  const float *xr = a0.x + long(rowOk ? row : 0) * a0.I;
+  const float *w[M];
+#pragma unroll
+  for (int e = 0; e < M; ++e) w[e] = a[e].w + long(a0.layer) * a0.I * a0.O + (colOk ? n : 0);
+  const int kb0 = min(kg * a0.kChunk, a0.I), kb1 = min(kb0 + a0.kChunk, a0.I);
 
-  floatx16 acc[J];
+  floatx16 acc[M][J];
 #pragma unroll
-  for (int j = 0; j < J; ++j)
+  for (int e = 0; e < M; ++e)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[j][r] = 0.f;
+    for (int j = 0; j < J; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[e][j][r] = 0.f;
 
   // The slice is cut into 16*S-row stages dealt round-robin to the 4 waves (wave w takes stages
   // w, w+4, ...), so the waves of a workgroup stream neighbouring weight rows at any moment.
@@ -564,76 +610,81 @@ template <MfmaFlavour F, int J, int S> __device__ void linear_mfma(const LinearA
   const int full = fullTotal > wave ? (fullTotal - wave + 3) / 4 : 0;
   const int k = kb0 + R * wave + 4 * s;                // this lane's row in the wave's first stage
   const int k1 = kb1;
-  MfmaStage<J, S> sa, sb;
+  const long O = a0.O;
+  MfmaStage<J, S, M> sa, sb;
   int t = 0;
-  if (full > 0) mfma_load<J, S, false>(sa, xr, w, a.O, k, k1);
+  if (full > 0) mfma_load<J, S, M, false>(sa, xr, w, O, k, k1);
   for (; t + 1 < full; t += 2) {
-    mfma_load<J, S, false>(sb, xr, w, a.O, k + 4 * R * (t + 1), k1);
+    mfma_load<J, S, M, false>(sb, xr, w, O, k + 4 * R * (t + 1), k1);
     __builtin_amdgcn_sched_barrier(0);
-    stage_compute<F, J, S>(sa, acc);
+    stage_compute<F, J, S, M>(sa, acc);
     __builtin_amdgcn_sched_barrier(0);
-    mfma_load<J, S, false>(sa, xr, w, a.O, k + 4 * R * min(t + 2, full - 1), k1);
+    mfma_load<J, S, M, false>(sa, xr, w, O, k + 4 * R * min(t + 2, full - 1), k1);
     __builtin_amdgcn_sched_barrier(0);
-    stage_compute<F, J, S>(sb, acc);
+    stage_compute<F, J, S, M>(sb, acc);
     __builtin_amdgcn_sched_barrier(0);
   }
-  if (t < full) stage_compute<F, J, S>(sa, acc);
+  if (t < full) stage_compute<F, J, S, M>(sa, acc);
   const int tailBase = kb0 + R * fullTotal;
   const int tailStages = (kb1 - tailBase + 15) / 16;
 #pragma unroll 1
   for (int q = (wave - fullTotal % 4 + 4) % 4; q < tailStages; q += 4) {
-    MfmaStage<J, 1> st;
-    mfma_load<J, 1, true>(st, xr, w, a.O, tailBase + 16 * q + 4 * s, k1);
-    stage_compute<F, J, 1>(st, acc);
+    MfmaStage<J, 1, M> st;
+    mfma_load<J, 1, M, true>(st, xr, w, O, tailBase + 16 * q + 4 * s, k1);
+    stage_compute<F, J, 1, M>(st, acc);
   }
 
   // Every wave hands its tile to the others through LDS; wave w then adds rows {8w + 4s + q} of
   // the tile (its accumulator registers 4w .. 4w+3) in wave order and stores them, so the four
-  // waves share the epilogue. Columns go through LDS in groups of JH (at most 2: 32 KB).
-  // Partial planes the consumer combines (deferred) are plain stores; planes combined here go
-  // through the agent-coherent path.
+  // waves share the epilogue. Columns go through LDS in groups of JH (at most 2: 32 KB), member
+  // after member. Partial planes the consumer combines (deferred) are plain stores; planes
+  // combined here go through the agent-coherent path.
   constexpr int JH = J < 2 ? J : 2;
-  const int rowTiles = (a.B + 31) / 32;
-  float *partial = split_partials(a, false);
+  const int rowTiles = (a0.B + 31) / 32;
 #pragma unroll
-  for (int h = 0; h < J; h += JH) {
-    if (h > 0) __syncthreads();
+  for (int e = 0; e < M; ++e) {
+    const LinearArgs &ae = a[e];
+    float *partial = split_partials(ae, false);
 #pragma unroll
-    for (int j = 0; j < JH; ++j)
+    for (int h = 0; h < J; h += JH) {
+      if (e > 0 || h > 0) __syncthreads();
 #pragma unroll
-      for (int r = 0; r < 16; ++r) smem[((wave * JH + j) * 16 + r) * 64 + lane] = acc[h + j][r];
-    __syncthreads();
+      for (int j = 0; j < JH; ++j)
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      float sum[JH];
+        for (int r = 0; r < 16; ++r) smem[((wave * JH + j) * 16 + r) * 64 + lane] = acc[e][h + j][r];
+      __syncthreads();
 #pragma unroll
-      for (int j = 0; j < JH; ++j) sum[j] = smem[(j * 16 + 4 * wave + q) * 64 + lane];
+      for (int q = 0; q < 4; ++q) {
+        float sum[JH];
 #pragma unroll
-      for (int v = 1; v < 4; ++v)
+        for (int j = 0; j < JH; ++j) sum[j] = smem[(j * 16 + 4 * wave + q) * 64 + lane];
 #pragma unroll
-        for (int j = 0; j < JH; ++j) sum[j] += smem[((v * JH + j) * 16 + 4 * wave + q) * 64 + lane];
-      const int i = rt * 32 + 8 * wave + 4 * s + q;   // row of accumulator register 4*wave + q
-      if (!colOk) continue;
-      if (a.kSplit > 1) {
-        float *p = partial + long(kg) * rowTiles * 32 * a.O + long(i) * a.O + n + h;
-        if (a.deferred) {
+        for (int v = 1; v < 4; ++v)
+#pragma unroll
+          for (int j = 0; j < JH; ++j) sum[j] += smem[((v * JH + j) * 16 + 4 * wave + q) * 64 + lane];
+        const int i = rt * 32 + 8 * wave + 4 * s + q;   // row of accumulator register 4*wave + q
+        if (!colOk) continue;
+        if (ae.kSplit > 1) {
+          float *p = partial + long(kg) * rowTiles * 32 * O + long(i) * O + n + h;
+          if (ae.deferred) {
+            if constexpr (JH == 2) *reinterpret_cast<float2 *>(p) = make_float2(sum[0], sum[1]);
+            else *p = sum[0];
+          } else {
+#pragma unroll
+            for (int j = 0; j < JH; ++j) partial_store(p + j, sum[j]);
+          }
+        } else if (i < ae.B) {
+          float *p = ae.dst + long(i) * O + n + h;
           if constexpr (JH == 2) *reinterpret_cast<float2 *>(p) = make_float2(sum[0], sum[1]);
           else *p = sum[0];
-        } else {
-#pragma unroll
-          for (int j = 0; j < JH; ++j) partial_store(p + j, sum[j]);
         }
-      } else if (i < a.B) {
-        float *p = a.dst + long(i) * a.O + n + h;
-        if constexpr (JH == 2) *reinterpret_cast<float2 *>(p) = make_float2(sum[0], sum[1]);
-        else *p = sum[0];
       }
     }
-  }
-  if (a.kSplit > 1 && !a.deferred) {
-    unsigned *counters = split_counters(a);
-    if (split_arrive(counters + rt * a.tilesN + tn, a.kSplit))
-      split_finish(a, partial, long(rowTiles) * 32 * a.O, rt * 32, 32, tn * 32 * J, 32 * J);
+    if (ae.kSplit > 1 && !ae.deferred) {
+      unsigned *counters = split_counters(ae);
+      if (split_arrive(counters + rt * ae.tilesN + tn, ae.kSplit))
+        split_finish(ae, partial, long(rowTiles) * 32 * O, rt * 32, 32, tn * 32 * J, 32 * J);
+    }
   }
 }
 
@@ -693,11 +744,11 @@ __device__ void linear_rowvec_body(const LinearArgs &a, int block) {
 
 template <int J, int S> __device__ void linear_mfma_body(const LinearArgs &a, int block) {
   extern __shared__ float smem[];
-  linear_mfma<MfmaFlavour::F32, J, S>(a, block, smem);
+  linear_mfma<MfmaFlavour::F32, J, S, 1>(&a, block, smem);
 }
 template <int J, int S> __device__ void linear_split_body(const LinearArgs &a, int block) {
   extern __shared__ float smem[];
-  linear_mfma<MfmaFlavour::SplitBf16, J, S>(a, block, smem);
+  linear_mfma<MfmaFlavour::SplitBf16, J, S, 1>(&a, block, smem);
 }
 CKL_ENTRY_ATTR(linear_rowvec, LinearArgs, linear_rowvec_body, 1024, )
 // ckl_linear_mfma<J>x<S>: J weight columns per lane, 16*S reduction rows per stage.
@@ -716,6 +767,22 @@ CKL_ENTRY_ATTR(linear_split2x1, LinearArgs, (linear_split_body<2, 1>), kBlock, C
 CKL_ENTRY_ATTR(linear_split2x2, LinearArgs, (linear_split_body<2, 2>), kBlock, CKL_TWO_WAVES)
 CKL_ENTRY_ATTR(linear_split4x1, LinearArgs, (linear_split_body<4, 1>), kBlock, CKL_TWO_WAVES)
 CKL_ENTRY_ATTR(linear_split4x2, LinearArgs, (linear_split_body<4, 2>), kBlock, CKL_TWO_WAVES)
+// ckl_linear_mfma<J>x1_shared<M>: M linears of one shape and tiling that multiply the same x
+// (their blocks in a Group<LinearArgs>, count == M; grid = one member's grid). Each workgroup
+// computes its tile of every member from one x stream, so the sibling projections of a decoder
+// layer (q, k, v; gate, up) run as one grid of at most one workgroup per CU.
+#define CKL_LINEAR_SHARED(J, M)                                                                       \
+  extern "C" __global__ __launch_bounds__(kBlock) CKL_ONE_WAVE void ckl_linear_mfma##J##x1_shared##M( \
+      const Group<LinearArgs> g) {                                                                    \
+    extern __shared__ float smem[];                                                                   \
+    linear_mfma<MfmaFlavour::F32, J, 1, M>(g.m, blockIdx.x, smem);                                    \
+  }
+CKL_LINEAR_SHARED(1, 2)
+CKL_LINEAR_SHARED(1, 3)
+CKL_LINEAR_SHARED(2, 2)
+CKL_LINEAR_SHARED(2, 3)
+CKL_LINEAR_SHARED(4, 2)
+CKL_LINEAR_SHARED(4, 3)
 
 // ------------------------------------------------------------------ rope
 // Adjacent-pair rotation at position p (workloads.py:72-85):
@@ -1023,40 +1090,64 @@ CKL_ENTRY_ATTR(softmax__attention_values, SoftmaxValuesChainArgs, softmax__atten
 // attention_scores does), the softmax in place in LDS, then the values from LDS. Scores and
 // probabilities are also written to global memory unless the executor cleared those pointers
 // (only the chain reads them).
-__device__ void attention_scores__softmax__attention_values_body(const AttentionChainArgs &a, int block) {
-  extern __shared__ float rowScores[];
-  const ScoresArgs &sc = a.scores;
-  long bh = block;
-  if (bh >= long(a.values.B) * a.values.A) return;
+// A wave's kScoreBatch cache-row loads of the scores' vector layout (groups of D/4 lanes hold one
+// row as float4s): rows base + u*rowsPerLoad + sub; rows past `end` re-read an early row.
+struct KeyBatch { float4 kv[kScoreBatch]; };
+struct KeyLayout {
+  int width, rowsPerLoad, sub, part;
+  __device__ explicit KeyLayout(int D) : width(D / 4), rowsPerLoad(64 / (D / 4)) {
+    const int lane = threadIdx.x & 63;
+    sub = lane / width;
+    part = lane % width;
+  }
+};
+__device__ __forceinline__ void load_key_batch(KeyBatch &kb, const float *keys, int D, const KeyLayout &k, int base,
+                                               int end) {
+#pragma unroll
+  for (int u = 0; u < kScoreBatch; ++u) {
+    int t = base + u * k.rowsPerLoad + k.sub;
+    t = t < end ? t : min(k.sub, end - 1);        // past the end: re-read an early row, dropped
+    kb.kv[u] = reinterpret_cast<const float4 *>(keys + long(t) * D)[k.part];
+  }
+}
+__device__ __forceinline__ void score_key_batch(const KeyBatch &kb, float4 qv, const KeyLayout &k, int base, int end,
+                                                float scale, float *rowScores, float *scores) {
+#pragma unroll
+  for (int u = 0; u < kScoreBatch; ++u) {
+    float v = group_sum(dot4(qv, kb.kv[u]), k.width) * scale;
+    int t = base + u * k.rowsPerLoad + k.sub;
+    if (k.part == 0 && t < end) {
+      rowScores[t] = v;
+      if (scores) scores[t] = v;
+    }
+  }
+}
+
+// The scores -> softmax -> values row of (b, h) = bh with the query row `q` (global memory, or
+// LDS in the rope chain): scores into rowScores (LDS, T floats), softmax in place, values. With
+// `haveFirst`, `first` holds the wave's first batch of cache rows (vector layout only).
+__device__ __forceinline__ void attention_chain_row(const ScoresArgs &sc, const SoftmaxArgs &softmax,
+                                                    const ValuesArgs &values, long bh, const float *q,
+                                                    float *rowScores, const KeyBatch &first, bool haveFirst) {
   int p = load_position(sc.position);
   int end = min(p + 1, sc.T);
   if (p < 0) end = 0;
-  const float *q = sc.q + bh * sc.D;
   const float *keys = sc.kc + (long(sc.layer) * sc.B * sc.A + bh) * long(sc.T) * sc.D;
   float *scores = sc.scores ? sc.scores + bh * sc.T : nullptr;
   if (scores_vector_layout(sc.D)) {
-    const int width = sc.D / 4, rowsPerLoad = 64 / width;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
-    const int sub = lane / width, part = lane % width;
-    const float4 qv = reinterpret_cast<const float4 *>(q)[part];
-    const int step = waves * kScoreBatch * rowsPerLoad;
-    for (int base = wave * kScoreBatch * rowsPerLoad; base < end; base += step) {
-      float4 kv[kScoreBatch];
-#pragma unroll
-      for (int u = 0; u < kScoreBatch; ++u) {
-        int t = base + u * rowsPerLoad + sub;
-        t = t < end ? t : min(sub, end - 1);      // past the end: re-read an early row, dropped
-        kv[u] = reinterpret_cast<const float4 *>(keys + long(t) * sc.D)[part];
-      }
-#pragma unroll
-      for (int u = 0; u < kScoreBatch; ++u) {
-        float v = group_sum(dot4(qv, kv[u]), width) * sc.scale;
-        int t = base + u * rowsPerLoad + sub;
-        if (part == 0 && t < end) {
-          rowScores[t] = v;
-          if (scores) scores[t] = v;
-        }
-      }
+    const KeyLayout k(sc.D);
+    const int wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
+    const float4 qv = reinterpret_cast<const float4 *>(q)[k.part];
+    const int step = waves * kScoreBatch * k.rowsPerLoad;
+    int base = wave * kScoreBatch * k.rowsPerLoad;
+    if (haveFirst) {
+      score_key_batch(first, qv, k, base, end, sc.scale, rowScores, scores);
+      base += step;
+    }
+    for (; base < end; base += step) {
+      KeyBatch kb;
+      load_key_batch(kb, keys, sc.D, k, base, end);
+      score_key_batch(kb, qv, k, base, end, sc.scale, rowScores, scores);
     }
   } else {
     for (int t = threadIdx.x; t < end; t += blockDim.x) {
@@ -1066,13 +1157,76 @@ __device__ void attention_scores__softmax__attention_values_body(const Attention
     }
   }
   __syncthreads();
-  const int rowThreads = a.softmax.rowThreads;
-  softmax_row(a.softmax, rowScores, bh, int(threadIdx.x) % rowThreads, int(threadIdx.x) < rowThreads, rowScores);
+  const int rowThreads = softmax.rowThreads;
+  softmax_row(softmax, rowScores, bh, int(threadIdx.x) % rowThreads, int(threadIdx.x) < rowThreads, rowScores);
   __syncthreads();
-  attention_values_row(a.values, bh, rowScores);
+  attention_values_row(values, bh, rowScores);
+}
+
+__device__ void attention_scores__softmax__attention_values_body(const AttentionChainArgs &a, int block) {
+  extern __shared__ float rowScores[];
+  long bh = block;
+  if (bh >= long(a.values.B) * a.values.A) return;
+  KeyBatch none;
+  attention_chain_row(a.scores, a.softmax, a.values, bh, a.scores.q + bh * a.scores.D, rowScores, none, false);
 }
 CKL_ENTRY_ATTR(attention_scores__softmax__attention_values, AttentionChainArgs,
                attention_scores__softmax__attention_values_body, kValuesBlock, )
+
+// rope(q), rope(k) -> append_kv -> attention_scores -> softmax -> attention_values as one launch
+// of attention_values's geometry: workgroup (b, h) first rotates its head's pairs of q and k at
+// the current position (as rope does), writes the rotated q (and k, unless only append reads it),
+// keeps the rotated q in LDS and appends the rotated k and v's row to the caches; once those
+// stores have completed (s_waitcnt vmcnt(0), then the workgroup barrier) it runs the attention row
+// as the attention chain does, with the query from LDS and the first batch of cache-row loads
+// issued before the rotation. The position is outside
+// [0, T) only if the caller lets it run past the cache capacity; then rope and append write
+// nothing and the attention reads q's buffer, as the separate dispatches would.
+// Dynamic LDS: the row of T scores (padded to 4 floats), then the D-float query.
+__device__ void rope__rope__append_kv__attention_scores__softmax__attention_values_body(
+    const RopeAttentionChainArgs &a, int block) {
+  extern __shared__ float rowScores[];
+  const RopeArgs &q = a.q, &k = a.k;
+  const AppendArgs &ap = a.append;
+  const ScoresArgs &sc = a.scores;
+  long bh = block;
+  if (bh >= long(a.values.B) * a.values.A) return;
+  float *qrow = rowScores + ((q.T + 3) & ~3);
+  const int p = load_position(q.position);
+  const bool inRange = p >= 0 && p < q.T;
+  // The first batch of every wave's cache rows lies below p when p >= the batch stride: those
+  // loads are issued before the rotation and overlap it (the rows are not written here).
+  const int wave = threadIdx.x >> 6;
+  const bool vector = scores_vector_layout(sc.D);
+  const KeyLayout layout(vector ? sc.D : 4);
+  const int firstBase = wave * kScoreBatch * layout.rowsPerLoad;
+  const bool early = vector && inRange && p >= int(blockDim.x >> 6) * kScoreBatch * layout.rowsPerLoad;
+  KeyBatch first;
+  if (early)
+    load_key_batch(first, sc.kc + (long(sc.layer) * sc.B * sc.A + bh) * long(sc.T) * sc.D, sc.D, layout, firstBase, p);
+  if (inRange) {
+    for (int r = threadIdx.x; r < q.R; r += blockDim.x) {
+      long c = bh * (2L * q.R) + 2 * r;              // = b*(2R*A) + h*2R + 2r
+      float2 cs = *reinterpret_cast<const float2 *>(q.table + (long(p) * q.R + r) * 2);
+      float2 qr = rotate(source2(a.qsrc, q.src, c), cs);
+      *reinterpret_cast<float2 *>(q.dst + c) = qr;
+      *reinterpret_cast<float2 *>(qrow + 2 * r) = qr;
+      float2 kr = rotate(source2(a.ksrc, k.src, c), cs);
+      if (k.dst) *reinterpret_cast<float2 *>(k.dst + c) = kr;
+      long row = (((long(ap.layer) * ap.B * ap.A) + bh) * ap.T + p) * ap.D + 2 * r;
+      *reinterpret_cast<float2 *>(ap.kc + row) = kr;
+      *reinterpret_cast<float2 *>(ap.vc + row) = source2(a.v, ap.v, c);
+    }
+  }
+  // The barrier alone does not wait for vector stores: waves that appended cache rows wait for
+  // them (and their loads) before other waves may load those rows.
+  if (inRange && int(threadIdx.x & ~63) < q.R) __builtin_amdgcn_s_waitcnt(kWaitStores);
+  __syncthreads();
+  attention_chain_row(a.scores, a.softmax, a.values, bh, inRange ? qrow : sc.q + bh * sc.D, rowScores, first,
+                      early);
+}
+CKL_ENTRY_ATTR(rope__rope__append_kv__attention_scores__softmax__attention_values, RopeAttentionChainArgs,
+               rope__rope__append_kv__attention_scores__softmax__attention_values_body, kValuesBlock, )
 
 // ------------------------------------------------------------------ pointwise
 // add: dst = x + y; multiply: dst = x * y; silu: dst = v / (1 + exp(-v)) (workloads.py:145-167).

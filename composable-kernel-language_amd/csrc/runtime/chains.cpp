@@ -4,8 +4,9 @@
 // most of the time of the decode step's row-local kernels. The kernel library therefore has chain
 // entry points (csrc/kernels/library.hip) that run several dependent dispatches row by row in one
 // grid: rms_stats -> rms_apply, add -> rms_stats -> rms_apply, embedding -> rms_stats ->
-// rms_apply, silu -> multiply, attention_scores -> softmax -> attention_values (or softmax ->
-// attention_values), rope(q), rope(k) -> append_kv and greedy -> advance. The plan itself (nodes, edges,
+// rms_apply, silu -> multiply, rope(q), rope(k) -> append_kv -> attention_scores -> softmax ->
+// attention_values (or the rope part alone, attention_scores -> softmax -> attention_values, or
+// softmax -> attention_values) and greedy -> advance. The plan itself (nodes, edges,
 // argument blocks) is unchanged; only the inferred lowering contracts a chain into one unit.
 //
 // A chain is taken only when
@@ -272,6 +273,58 @@ const char *ropeAppendChain(const Members &m, const Internal &internal, Launch &
   return nullptr;
 }
 
+// rope(q), rope(k) -> append_kv -> attention_scores -> softmax -> attention_values: the rope chain
+// and the attention chain of one layer, fused per (b, h). Every buffer is touched only in the
+// worker's (b, h) rows: q, k, v and the outputs in rows of D floats, the caches in slabs of T*D.
+const char *ropeAttentionChain(const Members &m, const Internal &internal, Launch &out) {
+  RopeAttentionChainArgs c{block<RopeArgs>(*m[0]),   block<RopeArgs>(*m[1]),    block<AppendArgs>(*m[2]),
+                           block<ScoresArgs>(*m[3]), block<SoftmaxArgs>(*m[4]), block<ValuesArgs>(*m[5]),
+                           {}, {}, {}};
+  const RopeArgs &q = c.q, &k = c.k;
+  const AppendArgs &ap = c.append;
+  const ScoresArgs &sc = c.scores;
+  const SoftmaxArgs &x = c.softmax;
+  const ValuesArgs &v = c.values;
+  const Launch &values = *m[5];
+  if (q.table != k.table || q.position != k.position || q.position != ap.position || q.B != k.B || q.A != k.A ||
+      q.R != k.R || q.T != k.T)
+    return "the two ropes disagree on table, position or shape";
+  if (ap.k != k.dst || ap.B != q.B || ap.A != q.A || ap.D != 2 * q.R || ap.T != q.T || ap.layer < 0 || ap.L <= ap.layer)
+    return "append_kv does not take the rotated k";
+  if (sc.q != q.dst || sc.kc != ap.kc || v.vc != ap.vc || sc.layer != ap.layer || v.layer != ap.layer)
+    return "the attention does not read the rotated q and the appended caches";
+  if (sc.scores != x.scores || x.probs != v.probs || sc.position != q.position || x.position != q.position ||
+      v.position != q.position)
+    return "softmax and attention_values do not consume the scores chain";
+  if (sc.B != q.B || sc.A != q.A || sc.T != q.T || sc.D != ap.D || x.B != q.B || x.A != q.A || x.T != q.T ||
+      v.B != q.B || v.A != q.A || v.T != q.T || v.D != ap.D || v.L != ap.L || sc.L != ap.L)
+    return "attention shapes disagree";
+  if (q.B <= 0 || q.A <= 0 || q.R <= 0 || q.T <= 0 || q.T > kChainSoftmaxRow)
+    return "attention row does not fit the chain's LDS copy";
+  if ((x.rowThreads != 64 && x.rowThreads != 256) || values.block[0] < unsigned(x.rowThreads))
+    return "attention_values workgroup is narrower than a softmax row";
+  if (values.grid[0] != unsigned(q.B) * unsigned(q.A)) return "attention_values grid is not one workgroup per row";
+  uint64_t bh = uint64_t(q.B) * uint64_t(q.A), head = 4ull * uint64_t(ap.D), row = 4ull * uint64_t(q.T);
+  uint64_t slab = uint64_t(q.T) * head, cache = bh * uint64_t(q.T) * uint64_t(ap.D);
+  if (internal(1, k.dst)) c.k.dst = nullptr;
+  if (internal(3, sc.scores)) c.scores.scores = nullptr;
+  if (internal(4, x.probs)) c.softmax.probs = nullptr;
+  std::vector<Range> ranges{rows(q.src, bh, head, false), rows(k.src, bh, head, false), rows(ap.v, bh, head, false),
+                            rows(q.dst, bh, head, true), whole(q.table, 8ull * uint64_t(q.T) * uint64_t(q.R)),
+                            whole(q.position, 4), rows(ap.kc + int64_t(ap.layer) * int64_t(cache), bh, slab, true),
+                            rows(ap.vc + int64_t(ap.layer) * int64_t(cache), bh, slab, true),
+                            rows(v.dst, bh, head, true)};
+  if (c.k.dst) ranges.push_back(rows(k.dst, bh, head, true));
+  if (c.scores.scores) ranges.push_back(rows(sc.scores, bh, row, true));
+  if (c.softmax.probs) ranges.push_back(rows(x.probs, bh, row, true));
+  if (!hazardFree(ranges)) return kOverlap;
+  out.grid[0] = values.grid[0];
+  out.block[0] = values.block[0];
+  out.shared = unsigned(16 * ((uint64_t(q.T) + 3) / 4) + head);   // T floats padded to a float4, then D floats
+  setArguments(out, c);
+  return nullptr;
+}
+
 const char *greedyAdvanceChain(const Members &m, const Internal &, Launch &out) {
   GreedyAdvanceChainArgs c{block<GreedyArgs>(*m[0]), block<AdvanceArgs>(*m[1])};
   const GreedyArgs &g = c.greedy;
@@ -327,6 +380,32 @@ std::vector<size_t> matchRopeAppend(const Plan &plan, size_t head, const Success
   return {head, k, appendOf(k)};
 }
 
+// The rope chain's three roles, then attention_scores taking the rotated q and reading the
+// appended cache, softmax of its scores and attention_values of its probabilities.
+std::vector<size_t> matchRopeAttention(const Plan &plan, size_t head, const Successors &successors,
+                                       const std::vector<bool> &taken) {
+  std::vector<size_t> roles = matchRopeAppend(plan, head, successors, taken);
+  if (roles.size() != 3) return {};
+  const void *rotatedQ = block<RopeArgs>(plan.nodes[roles[0]].launch).dst;
+  auto next = [&](size_t from, const char *name, auto accept) {
+    size_t found = plan.nodes.size();
+    for (size_t s : successors[from]) {
+      const Launch &l = plan.nodes[s].launch;
+      if (!taken[s] && l.name == name && singleGrid(l) && accept(l) && s < found) found = s;
+    }
+    return found;
+  };
+  const size_t n = plan.nodes.size();
+  size_t scores = next(roles[2], "ckl_attention_scores", [&](const Launch &l) { return block<ScoresArgs>(l).q == rotatedQ; });
+  if (scores == n) return {};
+  size_t softmax = next(scores, "ckl_softmax", [](const Launch &) { return true; });
+  if (softmax == n) return {};
+  size_t values = next(softmax, "ckl_attention_values", [](const Launch &) { return true; });
+  if (values == n) return {};
+  roles.insert(roles.end(), {scores, softmax, values});
+  return roles;
+}
+
 struct Rule {
   std::vector<std::string> members;   // entry points, in role order (dependency order for a path)
   const char *entry;                  // chain entry point
@@ -337,6 +416,11 @@ struct Rule {
 
 const std::vector<Rule> &rules() {
   static const std::vector<Rule> table = {
+      {{"ckl_rope", "ckl_rope", "ckl_append_kv", "ckl_attention_scores", "ckl_softmax", "ckl_attention_values"},
+       "ckl_rope__rope__append_kv__attention_scores__softmax__attention_values", ropeAttentionChain, matchRopeAttention,
+       {{0, offsetof(RopeArgs, src), offsetof(RopeAttentionChainArgs, qsrc)},
+        {1, offsetof(RopeArgs, src), offsetof(RopeAttentionChainArgs, ksrc)},
+        {2, offsetof(AppendArgs, v), offsetof(RopeAttentionChainArgs, v)}}},
       {{"ckl_add", "ckl_rms_stats", "ckl_rms_apply"}, "ckl_add__rms_stats__rms_apply", addRmsChain, nullptr,
        {{0, offsetof(BinaryArgs, x), offsetof(AddRmsChainArgs, x)}, {0, offsetof(BinaryArgs, y), offsetof(AddRmsChainArgs, y)}}},
       {{"ckl_embedding", "ckl_rms_stats", "ckl_rms_apply"}, "ckl_embedding__rms_stats__rms_apply", embeddingRmsChain},
@@ -492,6 +576,19 @@ std::vector<Chain> findChains(const Plan &plan, const std::vector<bool> &tempora
     }
   }
   return chains;
+}
+
+bool sharesOperands(const std::vector<const Launch *> &members) {
+  if (members.size() < 2 || members[0]->name.rfind("ckl_linear_mfma", 0) != 0) return false;
+  const LinearArgs a = block<LinearArgs>(*members[0]);
+  for (size_t k = 1; k < members.size(); ++k) {
+    if (members[k]->name != members[0]->name) return false;
+    const LinearArgs b = block<LinearArgs>(*members[k]);
+    if (b.x != a.x || b.B != a.B || b.I != a.I || b.O != a.O || b.layer != a.layer || b.tilesN != a.tilesN ||
+        b.kSplit != a.kSplit || b.kChunk != a.kChunk)
+      return false;
+  }
+  return true;
 }
 
 std::map<size_t, Launch> deferCombines(const Plan &plan, const std::vector<bool> &temporary, std::vector<Chain> &chains) {

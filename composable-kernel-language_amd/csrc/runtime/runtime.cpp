@@ -170,11 +170,15 @@ struct Unit {
   Launch launch;
 };
 
-Launch groupLaunch(const std::vector<const Launch *> &members) {
+// Group<Args> block of sibling launches. A shared-operand launch (`shared`) runs one member's grid
+// in which every workgroup serves all members; otherwise member m owns its own range of blocks.
+Launch groupLaunch(const std::vector<const Launch *> &members, bool shared) {
   const Launch &first = *members[0];
   Launch out = first;
-  out.function = first.groupFunction;
+  out.function = shared ? first.sharedFunction[members.size() - 2] : first.groupFunction;
   out.groupFunction = nullptr;
+  out.sharedFunction[0] = out.sharedFunction[1] = nullptr;
+  out.name = first.name + (shared ? "_shared" + std::to_string(members.size()) : std::string("_group"));
   size_t stride = first.arguments.size();
   std::vector<uint8_t> blob(kMaxGroup * stride + 4 * (kMaxGroup + 1) + 4, 0);
   int32_t start = 0;
@@ -191,7 +195,7 @@ Launch groupLaunch(const std::vector<const Launch *> &members) {
   std::memcpy(blob.data() + kMaxGroup * stride + 4 * (kMaxGroup + 1), &count, 4);
   blob.resize((blob.size() + 7) & ~size_t(7), 0);
   out.arguments = std::move(blob);
-  out.grid[0] = unsigned(start);
+  out.grid[0] = shared ? first.grid[0] : unsigned(start);
   return out;
 }
 
@@ -279,7 +283,9 @@ std::vector<Unit> groupPlan(const Plan &plan, const std::vector<Chain> &found, c
         g.members.insert(g.members.end(), base[u].members.begin(), base[u].members.end());
         launches.push_back(&base[u].launch);
       }
-      g.launch = groupLaunch(launches);
+      const bool shared = launches.size() <= 3 && launches[0]->sharedFunction[launches.size() - 2] &&
+                          sharesOperands(launches);
+      g.launch = groupLaunch(launches, shared);
       out.push_back(std::move(g));
     }
   }
@@ -673,6 +679,12 @@ extern "C" void ckl_kernel(void *frame, const char *name, uint64_t gx, uint64_t 
     std::string groupName = std::string(name) + "_group";
     if (hipModuleGetFunction(&group, f.module, groupName.c_str()) == hipSuccess) launch.groupFunction = group;
     else (void)hipGetLastError();
+    for (int m = 2; m <= 3; ++m) {
+      std::string sharedName = std::string(name) + "_shared" + std::to_string(m);
+      hipFunction_t shared = nullptr;
+      if (hipModuleGetFunction(&shared, f.module, sharedName.c_str()) == hipSuccess) launch.sharedFunction[m - 2] = shared;
+      else (void)hipGetLastError();
+    }
     uint64_t dims[6] = {gx, gy, gz, bx, by, bz};
     for (uint64_t d : dims)
       if (!d || d > 0xffffffffull) throw std::invalid_argument("kernel launch dimensions must be positive 32-bit values");

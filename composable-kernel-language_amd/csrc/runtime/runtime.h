@@ -57,6 +57,8 @@ struct Launch {
   hipModule_t module = nullptr;             // code object the function comes from
   hipFunction_t function = nullptr;
   hipFunction_t groupFunction = nullptr;   // sibling-group entry point, when the artifact has one
+  // Shared-operand entry points for 2 and 3 siblings (<name>_shared2, <name>_shared3).
+  hipFunction_t sharedFunction[2] = {nullptr, nullptr};
   std::string name;
   unsigned grid[3] = {1, 1, 1};
   unsigned block[3] = {1, 1, 1};
@@ -93,6 +95,9 @@ std::vector<Chain> findChains(const Plan &plan, const std::vector<bool> &tempora
 // Split linears whose every reader is a deferrable chain operand leave their combine to those
 // chains: returns the patched linear launches (by plan index) and fills the chains' sources.
 std::map<size_t, Launch> deferCombines(const Plan &plan, const std::vector<bool> &temporary, std::vector<Chain> &chains);
+// Whether sibling launches of one entry point read the same operand the way its _shared<M> entry
+// point requires (linears multiplying the same x with one shape and tiling).
+bool sharesOperands(const std::vector<const Launch *> &members);
 
 struct GraphExec {
   hipGraph_t graph = nullptr;

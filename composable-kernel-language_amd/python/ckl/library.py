@@ -258,18 +258,25 @@ def _rms_apply(shapes, consts, ext):
 # Tiling of the linear family (csrc/kernels/library.hip, "linear"): output tiles of 64 columns
 # (vector path) or 32*J columns (f32 MFMA path, 32 batch rows per tile), reduction slices of
 # k_chunk rows shared by the 4 waves of a workgroup, and k_split slices combined through the
-# workspace. Measured on MI355X (B = 32): a B = 32 f32 GEMV costs 16 MFMA FLOP per weight byte,
-# so one CU's MFMA rate covers ~38 GB/s of weights and the matrix has to be spread over most of
-# the 256 CUs; but every cross-workgroup split adds a coherent write/read round trip, and one
-# front sweeping the weight rows in address order streams best. The inferred graph hands the
-# split combine to the consuming chain kernel (csrc/runtime/chains.cpp), so splits there cost
-# only their partial planes. Measured inside the large decode step (weights not cached; a cold
-# streaming probe of these shapes needs >= ~700 workgroups in flight to pass 4.5 TB/s): J = 4
-# and no split for the LM head; J = 2 with 8 slices for square and down projections (I >= O)
-# and 4 slices for gate/up (O > I), slices of at least 256 rows. The vector path (B <= 16, latency-bound) runs one
-# workgroup per (64-column tile, batch row) whose up to 16 waves take 64 reduction rows each, all
-# loaded in one round trip; it splits only beyond 1024 rows.
-LINEAR_TARGET_GROUPS = 256
+# workspace. A B = 32 f32 GEMV costs 16 MFMA FLOP per weight byte, so the MFMA work is two thirds
+# of the HBM time and has to hide under the loads. Measured inside the large decode step on
+# MI355X (weights not cached), it does so only with one workgroup (one wave per SIMD) per CU:
+# with two or three workgroups per CU the MFMA and load phases of the waves sharing a SIMD stop
+# overlapping and a launch costs close to the sum of its MFMA-only and load-only times (gate/up
+# 33.6 us at 704 workgroups; 25.0 us on 176 workgroups), and a grid just over the CU count
+# doubles. So the MFMA path picks, in the order J = 2, 4, 1, the first tiling whose grid fills at
+# least LINEAR_MIN_FILL of LINEAR_TARGET_GROUPS workgroups without exceeding it (splitting K into
+# slices of at least LINEAR_MIN_CHUNK rows), else the fullest. Sibling linears that multiply the
+# same x (q/k/v, gate/up) then run in the inferred graph as one launch of the same grid in which
+# every workgroup serves all of them (ckl_linear_mfma<J>x1_shared<M>, csrc/runtime/runtime.cpp).
+# The inferred graph hands the split combine to the consuming chain kernel
+# (csrc/runtime/chains.cpp), so splits there cost only their partial planes. The vector path
+# (B <= 16, latency-bound) runs one workgroup per (64-column tile, batch row) whose up to 16
+# waves take 64 reduction rows each, all loaded in one round trip; it splits only beyond 1024
+# rows.
+LINEAR_TARGET_GROUPS = 256    # MI355X compute units
+LINEAR_MIN_FILL = 0.85
+LINEAR_MIN_CHUNK = 256
 LINEAR_ZERO_PAGE = 256    # kZeroPage: leading workspace bytes that stay zero
 LINEAR_VECTOR_ROWS = 16
 LINEAR_VECTOR_WAVES = 16      # waves per vector-path workgroup at most (1024 threads)
@@ -278,17 +285,24 @@ LINEAR_VECTOR_WAVE_ROWS = 64  # kVectorRows: reduction rows per wave
 
 def linear_tiling(b: int, i: int, o: int) -> dict:
     if b > LINEAR_VECTOR_ROWS and i % 4 == 0 and o % 4 == 0:
-        if o >= 16384:                  # LM head: 512 B of each weight row per wave, no split
-            j, split = 4, 1
-        else:                           # 64 columns per wave; 8 slices (I >= O) or 4 (gate/up)
-            j, split = 2, max(1, min(8 if i >= o else 4, i // 256))
-        tiles = _cdiv(o, 32 * j)
-        chunk = _cdiv(_cdiv(i, split), 16) * 16
-        split = _cdiv(i, chunk)
-        rows, row_tiles = _cdiv(b, 32) * 32, _cdiv(b, 32)
+        row_tiles = _cdiv(b, 32)
+        best = None
+        for j in (2, 4, 1):
+            tiles = _cdiv(o, 32 * j)
+            split = max(1, min(LINEAR_TARGET_GROUPS // (row_tiles * tiles), i // LINEAR_MIN_CHUNK))
+            chunk = _cdiv(_cdiv(i, split), 16) * 16
+            split = _cdiv(i, chunk)
+            grid = row_tiles * tiles * split
+            fill = grid / LINEAR_TARGET_GROUPS if grid <= LINEAR_TARGET_GROUPS else 0.5
+            if best is None or fill > best[0]:
+                best = (fill, j, tiles, split, chunk)
+            if fill >= LINEAR_MIN_FILL:
+                best = (fill, j, tiles, split, chunk)
+                break
+        _, j, tiles, split, chunk = best
+        rows = row_tiles * 32
         shared = 4 * min(j, 2) * 16 * 64 * 4          # the 4 waves' accumulator tiles, 2 columns at a time
-        stage = 1
-        entry = f"ckl_linear_mfma{j}x{stage}"
+        entry = f"ckl_linear_mfma{j}x1"
         block = BLOCK
     elif b <= LINEAR_VECTOR_ROWS:
         tiles = _cdiv(o, 64)

@@ -1,7 +1,7 @@
 """The linear kernel family on the GPU (benchmarks/decoder/workloads.py:61-69 body):
 dst[b, o] = sum_i x[b, i] * w[layer, i, o], against a float64 NumPy product.
 
-Shapes cover the vector path (B <= 16), both f32 MFMA paths (J = 1 and 4 columns per lane),
+Shapes cover the vector path (B <= 16), the f32 MFMA paths (J = 1, 2 and 4 columns per lane),
 split reductions across workgroups (the workspace and its completion counters, replayed so the
 self-resetting counters are exercised), ragged K/O/B tails and more than one 32-row batch
 tile. Tolerance: fp32 accumulation of I products of N(0, 1) inputs, |err| <= 1e-5 * sqrt(I)
@@ -32,7 +32,7 @@ _Y = ckl.Buffer[ckl.f32, (_B, _O)]
 
 @ckl.program
 def project(x: _X, w: _W, y: _Y, z: _Y, layer: ckl.constexpr[ckl.index]) -> None:
-    # Two independent projections: the inferred graph runs them as one sibling-group launch.
+    # Two projections of one x into caller buffers that may alias (so they run in order).
     ckl.launch(linear, x, w, y, layer, grid=(ckl.cdiv(_O, 64), _B), block=(64,))
     ckl.launch(linear, x, w, z, layer, grid=(ckl.cdiv(_O, 64), _B), block=(64,))
 
