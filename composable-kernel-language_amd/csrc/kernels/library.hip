@@ -95,6 +95,21 @@ __device__ __forceinline__ void wave_argmax(float &v, int &i) {
 
 __device__ __forceinline__ int load_position(const int *position) { return *position; }
 
+// Streaming loads: data a launch reads exactly once (weight rows, cache rows) is loaded with the
+// nontemporal cache policy (global_load ... nt). Measured on MI355X, per-workgroup contiguous
+// reads of a 2 GiB buffer stream at ~7.1 TB/s this way against ~6.1 TB/s with the default policy.
+typedef float stream_float4 __attribute__((ext_vector_type(4)));
+typedef float stream_float2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float4 stream_load4(const float *p) {
+  stream_float4 v = __builtin_nontemporal_load(reinterpret_cast<const stream_float4 *>(p));
+  return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ float2 stream_load2(const float *p) {
+  stream_float2 v = __builtin_nontemporal_load(reinterpret_cast<const stream_float2 *>(p));
+  return make_float2(v.x, v.y);
+}
+__device__ __forceinline__ float stream_load1(const float *p) { return __builtin_nontemporal_load(p); }
+
 // Operands of chain kernels that may be a split linear's partial planes (PartialSource, args.h):
 // the planes are added in g order starting from 0, as the linear's own combine (split_finish)
 // does, so deferring the combine leaves every value bit-identical. `i` is the element index.
@@ -425,13 +440,13 @@ __device__ void split_finish(const LinearArgs &a, const float *partial, long pla
 
 template <int J> __device__ __forceinline__ void load_columns(float (&out)[J], const float *p) {
   if constexpr (J == 4) {
-    float4 v = *reinterpret_cast<const float4 *>(p);
+    float4 v = stream_load4(p);
     out[0] = v.x; out[1] = v.y; out[2] = v.z; out[3] = v.w;
   } else if constexpr (J == 2) {
-    float2 v = *reinterpret_cast<const float2 *>(p);
+    float2 v = stream_load2(p);
     out[0] = v.x; out[1] = v.y;
   } else {
-    out[0] = *p;
+    out[0] = stream_load1(p);
   }
 }
 
@@ -718,13 +733,13 @@ __device__ void linear_rowvec_body(const LinearArgs &a, int block) {
   if (k1 - k0 == kVectorRows) {
     float wv[kVectorRows];
 #pragma unroll
-    for (int u = 0; u < kVectorRows; ++u) wv[u] = w[long(u) * a.O];
+    for (int u = 0; u < kVectorRows; ++u) wv[u] = stream_load1(w + long(u) * a.O);
 #pragma unroll
     for (int u = 0; u < kVectorRows; ++u) acc += xr[k0 + u] * wv[u];
   } else if (k0 < k1) {
     float wv[kVectorRows];
 #pragma unroll
-    for (int u = 0; u < kVectorRows; ++u) wv[u] = *(k0 + u < k1 ? w + long(u) * a.O : zero + lane);
+    for (int u = 0; u < kVectorRows; ++u) wv[u] = stream_load1(k0 + u < k1 ? w + long(u) * a.O : zero + lane);
 #pragma unroll
     for (int u = 0; u < kVectorRows; ++u) acc += (k0 + u < k1 ? xr[min(k0 + u, k1 - 1)] : 0.f) * wv[u];
   }
@@ -904,7 +919,7 @@ __device__ void attention_scores_body(const ScoresArgs &a, int block) {
       for (int u = 0; u < kScoreBatch; ++u) {
         int t = base + u * rowsPerLoad + sub;
         t = t < w1 ? t : min(w0 + sub, w1 - 1);    // past the end: re-read an early row, dropped
-        kv[u] = reinterpret_cast<const float4 *>(keys + long(t) * a.D)[part];
+        kv[u] = stream_load4(keys + long(t) * a.D + 4 * part);
       }
 #pragma unroll
       for (int u = 0; u < kScoreBatch; ++u) {
@@ -1029,7 +1044,7 @@ __device__ __forceinline__ void attention_values_row(const ValuesArgs &a, long b
       for (int u = 0; u < kValuesBatch; ++u) {
         int t = base + u * groups + g;
         int tc = t < end ? t : min(g, end - 1);    // past the end: re-read an early row, weight 0
-        v[u] = reinterpret_cast<const float4 *>(values + long(tc) * a.D)[part];
+        v[u] = stream_load4(values + long(tc) * a.D + 4 * part);
         pr[u] = t < end ? probs[tc] : 0.f;
       }
 #pragma unroll
@@ -1107,7 +1122,7 @@ __device__ __forceinline__ void load_key_batch(KeyBatch &kb, const float *keys, 
   for (int u = 0; u < kScoreBatch; ++u) {
     int t = base + u * k.rowsPerLoad + k.sub;
     t = t < end ? t : min(k.sub, end - 1);        // past the end: re-read an early row, dropped
-    kb.kv[u] = reinterpret_cast<const float4 *>(keys + long(t) * D)[k.part];
+    kb.kv[u] = stream_load4(keys + long(t) * D + 4 * k.part);
   }
 }
 __device__ __forceinline__ void score_key_batch(const KeyBatch &kb, float4 qv, const KeyLayout &k, int base, int end,
