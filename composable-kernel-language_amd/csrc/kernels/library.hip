@@ -960,9 +960,9 @@ template <bool IsMax> __device__ __forceinline__ float row_reduce(float v, int r
 // local index `local` < rowThreads (inactive lanes only take part in the synchronization).
 // Probabilities go to a.probs (unless null) and, when `stage` is given, to stage[t] as well;
 // `stage` may be `s` itself: every lane reads its elements before it writes them.
+// `p` is the position (a.position[0]), loaded by the caller.
 __device__ __forceinline__ void softmax_row(const SoftmaxArgs &a, const float *s, long row, int local, bool active,
-                                            float *stage) {
-  int p = load_position(a.position);
+                                            float *stage, int p) {
   int end = min(p + 1, a.T);
   if (p < 0) end = 0;
   float *out = a.probs ? a.probs + (active ? row : 0) * a.T : nullptr;   // null in a chain: LDS only
@@ -1014,7 +1014,7 @@ __device__ void softmax_body(const SoftmaxArgs &a, int block) {
   const int local = threadIdx.x % a.rowThreads;
   long row = long(block) * rowsPerBlock + threadIdx.x / a.rowThreads;
   const bool active = row < long(a.B) * a.A;       // uniform per row group (rowThreads divides kBlock)
-  softmax_row(a, a.scores + (active ? row : 0) * a.T, row, local, active, nullptr);
+  softmax_row(a, a.scores + (active ? row : 0) * a.T, row, local, active, nullptr, load_position(a.position));
 }
 CKL_ENTRY(softmax, SoftmaxArgs, softmax_body)
 
@@ -1026,34 +1026,58 @@ CKL_ENTRY(softmax, SoftmaxArgs, softmax_body)
 // sums are combined by a fixed-order tree in LDS. `probs` is the (b, h) row of probabilities
 // (global memory, or LDS in the softmax chain).
 constexpr int kValuesBatch = 8;
-__device__ __forceinline__ void attention_values_row(const ValuesArgs &a, long bh, const float *probs) {
+__device__ __forceinline__ bool values_vector_layout(int D) { return (D & 3) == 0 && D <= 4 * 64 && (64 % (D / 4)) == 0; }
+// A thread's kValuesBatch cache-row loads of the values' vector layout, rows base + u*groups + g
+// (rows past `end` re-read an early row; end > 0).
+struct ValueBatch { float4 v[kValuesBatch]; };
+__device__ __forceinline__ void load_value_batch(ValueBatch &vb, const float *values, int D, int base, int end) {
+  const int width = D / 4, groups = int(blockDim.x) / width;
+  const int g = threadIdx.x / width, part = threadIdx.x % width;
+#pragma unroll
+  for (int u = 0; u < kValuesBatch; ++u) {
+    int t = base + u * groups + g;
+    int tc = t < end ? t : min(g, end - 1);        // past the end: re-read an early row, weight 0
+    vb.v[u] = stream_load4(values + long(tc) * D + 4 * part);
+  }
+}
+__device__ __forceinline__ const float *values_slab(const ValuesArgs &a, long bh) {
+  return a.vc + (long(a.layer) * a.B * a.A + bh) * long(a.T) * a.D;
+}
+// `haveFirst`: `first` holds this thread's first batch (vector layout, end > 0). `p` is the
+// position (a.position[0]), loaded by the caller.
+__device__ __forceinline__ void attention_values_row(const ValuesArgs &a, long bh, const float *probs,
+                                                     const ValueBatch &first, bool haveFirst, int p) {
   __shared__ float4 partial[kValuesBlock];
-  int p = load_position(a.position);
   int end = min(p + 1, a.T);
   if (p < 0) end = 0;
-  const float *values = a.vc + (long(a.layer) * a.B * a.A + bh) * long(a.T) * a.D;
+  const float *values = values_slab(a, bh);
   float *dst = a.dst + bh * a.D;
-  if ((a.D & 3) == 0 && a.D <= 4 * 64 && (64 % (a.D / 4)) == 0) {
+  if (values_vector_layout(a.D)) {
     const int width = a.D / 4, groups = int(blockDim.x) / width;
     const int g = threadIdx.x / width, part = threadIdx.x % width;
+    const int step = kValuesBatch * groups;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int base = 0; base < end; base += kValuesBatch * groups) {
-      float4 v[kValuesBatch];
-      float pr[kValuesBatch];
+    auto consume = [&](const ValueBatch &vb, int base) {
 #pragma unroll
       for (int u = 0; u < kValuesBatch; ++u) {
         int t = base + u * groups + g;
-        int tc = t < end ? t : min(g, end - 1);    // past the end: re-read an early row, weight 0
-        v[u] = stream_load4(values + long(tc) * a.D + 4 * part);
-        pr[u] = t < end ? probs[tc] : 0.f;
+        int tc = t < end ? t : min(g, end - 1);
+        float pr = t < end ? probs[tc] : 0.f;
+        acc.x = __builtin_fmaf(pr, vb.v[u].x, acc.x);
+        acc.y = __builtin_fmaf(pr, vb.v[u].y, acc.y);
+        acc.z = __builtin_fmaf(pr, vb.v[u].z, acc.z);
+        acc.w = __builtin_fmaf(pr, vb.v[u].w, acc.w);
       }
-#pragma unroll
-      for (int u = 0; u < kValuesBatch; ++u) {
-        acc.x = __builtin_fmaf(pr[u], v[u].x, acc.x);
-        acc.y = __builtin_fmaf(pr[u], v[u].y, acc.y);
-        acc.z = __builtin_fmaf(pr[u], v[u].z, acc.z);
-        acc.w = __builtin_fmaf(pr[u], v[u].w, acc.w);
-      }
+    };
+    int base = 0;
+    if (haveFirst) {
+      consume(first, 0);
+      base = step;
+    }
+    for (; base < end; base += step) {
+      ValueBatch vb;
+      load_value_batch(vb, values, a.D, base, end);
+      consume(vb, base);
     }
     partial[threadIdx.x] = acc;
     __syncthreads();
@@ -1078,7 +1102,8 @@ __device__ __forceinline__ void attention_values_row(const ValuesArgs &a, long b
 __device__ void attention_values_body(const ValuesArgs &a, int block) {
   long bh = block;
   if (bh >= long(a.B) * a.A) return;
-  attention_values_row(a, bh, a.probs + bh * a.T);
+  ValueBatch none;
+  attention_values_row(a, bh, a.probs + bh * a.T, none, false, load_position(a.position));
 }
 CKL_ENTRY_ATTR(attention_values, ValuesArgs, attention_values_body, kValuesBlock, )
 
@@ -1093,9 +1118,10 @@ __device__ void softmax__attention_values_body(const SoftmaxValuesChainArgs &a, 
   if (bh >= long(a.values.B) * a.values.A) return;
   const int rowThreads = a.softmax.rowThreads;
   softmax_row(a.softmax, a.softmax.scores + bh * a.softmax.T, bh, int(threadIdx.x) % rowThreads,
-              int(threadIdx.x) < rowThreads, rowProbs);
+              int(threadIdx.x) < rowThreads, rowProbs, load_position(a.softmax.position));
   __syncthreads();
-  attention_values_row(a.values, bh, rowProbs);
+  ValueBatch none;
+  attention_values_row(a.values, bh, rowProbs, none, false, load_position(a.values.position));
 }
 CKL_ENTRY_ATTR(softmax__attention_values, SoftmaxValuesChainArgs, softmax__attention_values_body, kValuesBlock, )
 
@@ -1140,29 +1166,44 @@ __device__ __forceinline__ void score_key_batch(const KeyBatch &kb, float4 qv, c
 
 // The scores -> softmax -> values row of (b, h) = bh with the query row `q` (global memory, or
 // LDS in the rope chain): scores into rowScores (LDS, T floats), softmax in place, values. With
-// `haveFirst`, `first` holds the wave's first batch of cache rows (vector layout only).
+// `haveFirst`, `first` holds the wave's first batch of cache rows (vector layout only). With
+// `appended` (the rope chain, position in range), the key row at the position is read from LDS
+// instead of the cache and `storesPending` waves wait for their cache-row stores before the
+// barrier that precedes the values. The first batch of value rows is loaded before the softmax.
 __device__ __forceinline__ void attention_chain_row(const ScoresArgs &sc, const SoftmaxArgs &softmax,
                                                     const ValuesArgs &values, long bh, const float *q,
-                                                    float *rowScores, const KeyBatch &first, bool haveFirst) {
+                                                    float *rowScores, const KeyBatch &first, bool haveFirst,
+                                                    const float *appended = nullptr, bool storesPending = false) {
   int p = load_position(sc.position);
   int end = min(p + 1, sc.T);
   if (p < 0) end = 0;
   const float *keys = sc.kc + (long(sc.layer) * sc.B * sc.A + bh) * long(sc.T) * sc.D;
   float *scores = sc.scores ? sc.scores + bh * sc.T : nullptr;
-  if (scores_vector_layout(sc.D)) {
+  const bool vector = scores_vector_layout(sc.D);
+  if (vector) {
     const KeyLayout k(sc.D);
     const int wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
     const float4 qv = reinterpret_cast<const float4 *>(q)[k.part];
     const int step = waves * kScoreBatch * k.rowsPerLoad;
+    const int endG = appended ? end - 1 : end;       // the appended row comes from LDS
     int base = wave * kScoreBatch * k.rowsPerLoad;
     if (haveFirst) {
-      score_key_batch(first, qv, k, base, end, sc.scale, rowScores, scores);
+      score_key_batch(first, qv, k, base, endG, sc.scale, rowScores, scores);
       base += step;
     }
-    for (; base < end; base += step) {
+    for (; base < endG; base += step) {
       KeyBatch kb;
-      load_key_batch(kb, keys, sc.D, k, base, end);
-      score_key_batch(kb, qv, k, base, end, sc.scale, rowScores, scores);
+      load_key_batch(kb, keys, sc.D, k, base, endG);
+      score_key_batch(kb, qv, k, base, endG, sc.scale, rowScores, scores);
+    }
+    if (appended && wave == 0) {
+      // The row's score with the arithmetic of the cache path (any lane group reduces alike).
+      const float4 kv = reinterpret_cast<const float4 *>(appended)[k.part];
+      float v = group_sum(dot4(qv, kv), k.width) * sc.scale;
+      if ((threadIdx.x & 63) == 0) {
+        rowScores[p] = v;
+        if (scores) scores[p] = v;
+      }
     }
   } else {
     for (int t = threadIdx.x; t < end; t += blockDim.x) {
@@ -1171,11 +1212,15 @@ __device__ __forceinline__ void attention_chain_row(const ScoresArgs &sc, const 
       if (scores) scores[t] = v;
     }
   }
+  if (storesPending) __builtin_amdgcn_s_waitcnt(kWaitStores);
   __syncthreads();
+  ValueBatch vfirst;
+  const bool haveV = values_vector_layout(values.D) && end > 0;
+  if (haveV) load_value_batch(vfirst, values_slab(values, bh), values.D, 0, end);
   const int rowThreads = softmax.rowThreads;
-  softmax_row(softmax, rowScores, bh, int(threadIdx.x) % rowThreads, int(threadIdx.x) < rowThreads, rowScores);
+  softmax_row(softmax, rowScores, bh, int(threadIdx.x) % rowThreads, int(threadIdx.x) < rowThreads, rowScores, p);
   __syncthreads();
-  attention_values_row(values, bh, rowScores);
+  attention_values_row(values, bh, rowScores, vfirst, haveV, p);
 }
 
 __device__ void attention_scores__softmax__attention_values_body(const AttentionChainArgs &a, int block) {
@@ -1191,13 +1236,13 @@ CKL_ENTRY_ATTR(attention_scores__softmax__attention_values, AttentionChainArgs,
 // rope(q), rope(k) -> append_kv -> attention_scores -> softmax -> attention_values as one launch
 // of attention_values's geometry: workgroup (b, h) first rotates its head's pairs of q and k at
 // the current position (as rope does), writes the rotated q (and k, unless only append reads it),
-// keeps the rotated q in LDS and appends the rotated k and v's row to the caches; once those
-// stores have completed (s_waitcnt vmcnt(0), then the workgroup barrier) it runs the attention row
-// as the attention chain does, with the query from LDS and the first batch of cache-row loads
-// issued before the rotation. The position is outside
+// keeps the rotated q and k in LDS and appends the rotated k and v's row to the caches; then it
+// runs the attention row as the attention chain does, with the query and the appended key row
+// from LDS, the first batch of cache-row loads issued before the rotation, and the appending waves
+// waiting for their stores before the values read the cache. The position is outside
 // [0, T) only if the caller lets it run past the cache capacity; then rope and append write
 // nothing and the attention reads q's buffer, as the separate dispatches would.
-// Dynamic LDS: the row of T scores (padded to 4 floats), then the D-float query.
+// Dynamic LDS: the row of T scores (padded to 4 floats), then the D-float query and key rows.
 __device__ void rope__rope__append_kv__attention_scores__softmax__attention_values_body(
     const RopeAttentionChainArgs &a, int block) {
   extern __shared__ float rowScores[];
@@ -1207,6 +1252,7 @@ __device__ void rope__rope__append_kv__attention_scores__softmax__attention_valu
   long bh = block;
   if (bh >= long(a.values.B) * a.values.A) return;
   float *qrow = rowScores + ((q.T + 3) & ~3);
+  float *krow = qrow + ap.D;
   const int p = load_position(q.position);
   const bool inRange = p >= 0 && p < q.T;
   // The first batch of every wave's cache rows lies below p when p >= the batch stride: those
@@ -1228,17 +1274,17 @@ __device__ void rope__rope__append_kv__attention_scores__softmax__attention_valu
       *reinterpret_cast<float2 *>(qrow + 2 * r) = qr;
       float2 kr = rotate(source2(a.ksrc, k.src, c), cs);
       if (k.dst) *reinterpret_cast<float2 *>(k.dst + c) = kr;
+      *reinterpret_cast<float2 *>(krow + 2 * r) = kr;
       long row = (((long(ap.layer) * ap.B * ap.A) + bh) * ap.T + p) * ap.D + 2 * r;
       *reinterpret_cast<float2 *>(ap.kc + row) = kr;
       *reinterpret_cast<float2 *>(ap.vc + row) = source2(a.v, ap.v, c);
     }
   }
-  // The barrier alone does not wait for vector stores: waves that appended cache rows wait for
-  // them (and their loads) before other waves may load those rows.
-  if (inRange && int(threadIdx.x & ~63) < q.R) __builtin_amdgcn_s_waitcnt(kWaitStores);
   __syncthreads();
+  // The barrier alone does not wait for vector stores: the waves that appended cache rows wait for
+  // them before the barrier that precedes the values (the scores take the key row from LDS).
   attention_chain_row(a.scores, a.softmax, a.values, bh, inRange ? qrow : sc.q + bh * sc.D, rowScores, first,
-                      early);
+                      early, inRange ? krow : nullptr, inRange && int(threadIdx.x & ~63) < q.R);
 }
 CKL_ENTRY_ATTR(rope__rope__append_kv__attention_scores__softmax__attention_values, RopeAttentionChainArgs,
                rope__rope__append_kv__attention_scores__softmax__attention_values_body, kValuesBlock, )

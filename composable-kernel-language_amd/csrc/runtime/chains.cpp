@@ -320,7 +320,7 @@ const char *ropeAttentionChain(const Members &m, const Internal &internal, Launc
   if (!hazardFree(ranges)) return kOverlap;
   out.grid[0] = values.grid[0];
   out.block[0] = values.block[0];
-  out.shared = unsigned(16 * ((uint64_t(q.T) + 3) / 4) + head);   // T floats padded to a float4, then D floats
+  out.shared = unsigned(16 * ((uint64_t(q.T) + 3) / 4) + 2 * head);   // T floats padded to a float4, then 2 x D
   setArguments(out, c);
   return nullptr;
 }
