@@ -99,6 +99,10 @@ struct CKL_ALIGN RopeAttentionChainArgs {
   PartialSource qsrc, ksrc, v;
 };
 
+// Entry points named <entry>_nt read their streamed operand (weights, the cache) with
+// nontemporal loads; the executor selects them when that operand is at least this large.
+constexpr int64_t kStreamBytes = int64_t(8) << 20;
+
 // Largest row (in floats) an attention chain keeps in LDS.
 constexpr int kChainSoftmaxRow = 8192;
 

@@ -95,20 +95,34 @@ __device__ __forceinline__ void wave_argmax(float &v, int &i) {
 
 __device__ __forceinline__ int load_position(const int *position) { return *position; }
 
-// Streaming loads: data a launch reads exactly once (weight rows, cache rows) is loaded with the
-// nontemporal cache policy (global_load ... nt). Measured on MI355X, per-workgroup contiguous
-// reads of a 2 GiB buffer stream at ~7.1 TB/s this way against ~6.1 TB/s with the default policy.
+// Streaming loads: the `_nt` entry points read the data a launch reads exactly once (weight rows,
+// cache rows) with the nontemporal cache policy (global_load ... nt); the executor selects them
+// when that data is at least kStreamBytes (args.h). Measured on MI355X, per-workgroup contiguous
+// reads of a 2 GiB buffer stream at ~7.1 TB/s this way against ~6.1 TB/s with the default
+// policy; but a decode step whose few MB of weights stay in the caches between steps runs
+// slower with it, and a branch between the two in one kernel costs the small launches too.
 typedef float stream_float4 __attribute__((ext_vector_type(4)));
 typedef float stream_float2 __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ float4 stream_load4(const float *p) {
-  stream_float4 v = __builtin_nontemporal_load(reinterpret_cast<const stream_float4 *>(p));
-  return make_float4(v.x, v.y, v.z, v.w);
+template <bool NT> __device__ __forceinline__ float4 load4(const float *p) {
+  if constexpr (NT) {
+    stream_float4 v = __builtin_nontemporal_load(reinterpret_cast<const stream_float4 *>(p));
+    return make_float4(v.x, v.y, v.z, v.w);
+  } else {
+    return *reinterpret_cast<const float4 *>(p);
+  }
 }
-__device__ __forceinline__ float2 stream_load2(const float *p) {
-  stream_float2 v = __builtin_nontemporal_load(reinterpret_cast<const stream_float2 *>(p));
-  return make_float2(v.x, v.y);
+template <bool NT> __device__ __forceinline__ float2 load2(const float *p) {
+  if constexpr (NT) {
+    stream_float2 v = __builtin_nontemporal_load(reinterpret_cast<const stream_float2 *>(p));
+    return make_float2(v.x, v.y);
+  } else {
+    return *reinterpret_cast<const float2 *>(p);
+  }
 }
-__device__ __forceinline__ float stream_load1(const float *p) { return __builtin_nontemporal_load(p); }
+template <bool NT> __device__ __forceinline__ float load1(const float *p) {
+  if constexpr (NT) return __builtin_nontemporal_load(p);
+  else return *p;
+}
 
 // Operands of chain kernels that may be a split linear's partial planes (PartialSource, args.h):
 // the planes are added in g order starting from 0, as the linear's own combine (split_finish)
@@ -438,15 +452,15 @@ __device__ void split_finish(const LinearArgs &a, const float *partial, long pla
   }
 }
 
-template <int J> __device__ __forceinline__ void load_columns(float (&out)[J], const float *p) {
+template <int J, bool NT> __device__ __forceinline__ void load_columns(float (&out)[J], const float *p) {
   if constexpr (J == 4) {
-    float4 v = stream_load4(p);
+    float4 v = load4<NT>(p);
     out[0] = v.x; out[1] = v.y; out[2] = v.z; out[3] = v.w;
   } else if constexpr (J == 2) {
-    float2 v = stream_load2(p);
+    float2 v = load2<NT>(p);
     out[0] = v.x; out[1] = v.y;
   } else {
-    out[0] = stream_load1(p);
+    out[0] = load1<NT>(p);
   }
 }
 
@@ -463,7 +477,7 @@ template <int J, int S, int M> struct MfmaStage {
   float w[M][2 * S][4][J];
 };
 
-template <int J, int S, int M, bool Tail>
+template <int J, int S, int M, bool Tail, bool NT>
 __device__ __forceinline__ void mfma_load(MfmaStage<J, S, M> &st, const float *xr, const float *const (&w)[M], long O,
                                           int k, int k1) {
 #pragma unroll
@@ -482,13 +496,13 @@ __device__ __forceinline__ void mfma_load(MfmaStage<J, S, M> &st, const float *x
 #pragma unroll
         for (int m = 0; m < M; ++m) {
           float c[J];
-          load_columns<J>(c, w[m] + long(kr) * O);
+          load_columns<J, NT>(c, w[m] + long(kr) * O);
 #pragma unroll
           for (int j = 0; j < J; ++j) st.w[m][u][i][j] = inside ? c[j] : 0.f;
         }
       } else {
 #pragma unroll
-        for (int m = 0; m < M; ++m) load_columns<J>(st.w[m][u][i], w[m] + long(kk + i) * O);
+        for (int m = 0; m < M; ++m) load_columns<J, NT>(st.w[m][u][i], w[m] + long(kk + i) * O);
       }
     }
   }
@@ -586,7 +600,7 @@ __device__ __forceinline__ void stage_compute(const MfmaStage<J, S, M> &st, floa
 
 // `a` holds M member blocks that agree on x, B, I, O, layer and the tiling (M = 1: one linear);
 // the workgroup computes its tile of every member from one stream of x fragments.
-template <MfmaFlavour F, int J, int S, int M>
+template <MfmaFlavour F, int J, int S, int M, bool NT>
 __device__ void linear_mfma(const LinearArgs *a, int block, float *smem) {
   const LinearArgs &a0 = a[0];
   const int lane = threadIdx.x & 63;
@@ -628,13 +642,13 @@ __device__ void linear_mfma(const LinearArgs *a, int block, float *smem) {
   const long O = a0.O;
   MfmaStage<J, S, M> sa, sb;
   int t = 0;
-  if (full > 0) mfma_load<J, S, M, false>(sa, xr, w, O, k, k1);
+  if (full > 0) mfma_load<J, S, M, false, NT>(sa, xr, w, O, k, k1);
   for (; t + 1 < full; t += 2) {
-    mfma_load<J, S, M, false>(sb, xr, w, O, k + 4 * R * (t + 1), k1);
+    mfma_load<J, S, M, false, NT>(sb, xr, w, O, k + 4 * R * (t + 1), k1);
     __builtin_amdgcn_sched_barrier(0);
     stage_compute<F, J, S, M>(sa, acc);
     __builtin_amdgcn_sched_barrier(0);
-    mfma_load<J, S, M, false>(sa, xr, w, O, k + 4 * R * min(t + 2, full - 1), k1);
+    mfma_load<J, S, M, false, NT>(sa, xr, w, O, k + 4 * R * min(t + 2, full - 1), k1);
     __builtin_amdgcn_sched_barrier(0);
     stage_compute<F, J, S, M>(sb, acc);
     __builtin_amdgcn_sched_barrier(0);
@@ -645,7 +659,7 @@ __device__ void linear_mfma(const LinearArgs *a, int block, float *smem) {
 #pragma unroll 1
   for (int q = (wave - fullTotal % 4 + 4) % 4; q < tailStages; q += 4) {
     MfmaStage<J, 1, M> st;
-    mfma_load<J, 1, M, true>(st, xr, w, O, tailBase + 16 * q + 4 * s, k1);
+    mfma_load<J, 1, M, true, NT>(st, xr, w, O, tailBase + 16 * q + 4 * s, k1);
     stage_compute<F, J, 1, M>(st, acc);
   }
 
@@ -714,7 +728,7 @@ __device__ void linear_mfma(const LinearArgs *a, int block, float *smem) {
 // across workgroups.
 constexpr int kVectorRows = 64;
 constexpr int kVectorWaves = 16;
-__device__ void linear_rowvec_body(const LinearArgs &a, int block) {
+template <bool NT> __device__ void linear_rowvec_stream(const LinearArgs &a, int block) {
   __shared__ float red[kVectorWaves][64];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -733,13 +747,13 @@ __device__ void linear_rowvec_body(const LinearArgs &a, int block) {
   if (k1 - k0 == kVectorRows) {
     float wv[kVectorRows];
 #pragma unroll
-    for (int u = 0; u < kVectorRows; ++u) wv[u] = stream_load1(w + long(u) * a.O);
+    for (int u = 0; u < kVectorRows; ++u) wv[u] = load1<NT>(w + long(u) * a.O);
 #pragma unroll
     for (int u = 0; u < kVectorRows; ++u) acc += xr[k0 + u] * wv[u];
   } else if (k0 < k1) {
     float wv[kVectorRows];
 #pragma unroll
-    for (int u = 0; u < kVectorRows; ++u) wv[u] = stream_load1(k0 + u < k1 ? w + long(u) * a.O : zero + lane);
+    for (int u = 0; u < kVectorRows; ++u) wv[u] = load1<NT>(k0 + u < k1 ? w + long(u) * a.O : zero + lane);
 #pragma unroll
     for (int u = 0; u < kVectorRows; ++u) acc += (k0 + u < k1 ? xr[min(k0 + u, k1 - 1)] : 0.f) * wv[u];
   }
@@ -757,23 +771,27 @@ __device__ void linear_rowvec_body(const LinearArgs &a, int block) {
     split_finish(a, split_partials(a, true), long(a.B) * a.O, b, 1, tn * 64, 64);
 }
 
-template <int J, int S> __device__ void linear_mfma_body(const LinearArgs &a, int block) {
+template <int J, int S, bool NT = false> __device__ void linear_mfma_body(const LinearArgs &a, int block) {
   extern __shared__ float smem[];
-  linear_mfma<MfmaFlavour::F32, J, S, 1>(&a, block, smem);
+  linear_mfma<MfmaFlavour::F32, J, S, 1, NT>(&a, block, smem);
 }
 template <int J, int S> __device__ void linear_split_body(const LinearArgs &a, int block) {
   extern __shared__ float smem[];
-  linear_mfma<MfmaFlavour::SplitBf16, J, S, 1>(&a, block, smem);
+  linear_mfma<MfmaFlavour::SplitBf16, J, S, 1, false>(&a, block, smem);
 }
-CKL_ENTRY_ATTR(linear_rowvec, LinearArgs, linear_rowvec_body, 1024, )
+CKL_ENTRY_ATTR(linear_rowvec, LinearArgs, linear_rowvec_stream<false>, 1024, )
+CKL_ENTRY_ATTR(linear_rowvec_nt, LinearArgs, linear_rowvec_stream<true>, 1024, )
 // ckl_linear_mfma<J>x<S>: J weight columns per lane, 16*S reduction rows per stage.
 CKL_ENTRY(linear_mfma1x1, LinearArgs, (linear_mfma_body<1, 1>))
+CKL_ENTRY(linear_mfma1x1_nt, LinearArgs, (linear_mfma_body<1, 1, true>))
 CKL_ENTRY(linear_mfma1x2, LinearArgs, (linear_mfma_body<1, 2>))
 CKL_ENTRY_ATTR(linear_mfma1x4, LinearArgs, (linear_mfma_body<1, 4>), kBlock, CKL_TWO_WAVES)
 CKL_ENTRY(linear_mfma2x1, LinearArgs, (linear_mfma_body<2, 1>))
+CKL_ENTRY(linear_mfma2x1_nt, LinearArgs, (linear_mfma_body<2, 1, true>))
 CKL_ENTRY_ATTR(linear_mfma2x2, LinearArgs, (linear_mfma_body<2, 2>), kBlock, CKL_TWO_WAVES)
 CKL_ENTRY_ATTR(linear_mfma2x4, LinearArgs, (linear_mfma_body<2, 4>), kBlock, CKL_TWO_WAVES)
 CKL_ENTRY_ATTR(linear_mfma4x1, LinearArgs, (linear_mfma_body<4, 1>), kBlock, CKL_TWO_WAVES)
+CKL_ENTRY_ATTR(linear_mfma4x1_nt, LinearArgs, (linear_mfma_body<4, 1, true>), kBlock, CKL_TWO_WAVES)
 CKL_ENTRY_ATTR(linear_mfma4x2, LinearArgs, (linear_mfma_body<4, 2>), kBlock, CKL_TWO_WAVES)
 // ckl_linear_split<J>x<S>: the same tiling with the split-bf16 MFMA flavour.
 CKL_ENTRY(linear_split1x1, LinearArgs, (linear_split_body<1, 1>))
@@ -790,7 +808,12 @@ CKL_ENTRY_ATTR(linear_split4x2, LinearArgs, (linear_split_body<4, 2>), kBlock, C
   extern "C" __global__ __launch_bounds__(kBlock) CKL_ONE_WAVE void ckl_linear_mfma##J##x1_shared##M( \
       const Group<LinearArgs> g) {                                                                    \
     extern __shared__ float smem[];                                                                   \
-    linear_mfma<MfmaFlavour::F32, J, 1, M>(g.m, blockIdx.x, smem);                                    \
+    linear_mfma<MfmaFlavour::F32, J, 1, M, false>(g.m, blockIdx.x, smem);                             \
+  }                                                                                                   \
+  extern "C" __global__ __launch_bounds__(kBlock) CKL_ONE_WAVE void ckl_linear_mfma##J##x1_nt_shared##M( \
+      const Group<LinearArgs> g) {                                                                    \
+    extern __shared__ float smem[];                                                                   \
+    linear_mfma<MfmaFlavour::F32, J, 1, M, true>(g.m, blockIdx.x, smem);                              \
   }
 CKL_LINEAR_SHARED(1, 2)
 CKL_LINEAR_SHARED(1, 3)
@@ -893,7 +916,7 @@ __device__ __forceinline__ float score_scalar(const float *q, const float *key, 
   return v;
 }
 __device__ __forceinline__ bool scores_vector_layout(int D) { return (D & 3) == 0 && D <= 256 && (64 % (D / 4)) == 0; }
-__device__ void attention_scores_body(const ScoresArgs &a, int block) {
+template <bool NT> __device__ void attention_scores_body(const ScoresArgs &a, int block) {
   int chunks = (a.T + kBlock - 1) / kBlock;
   int chunk = block % chunks;
   long bh = block / chunks;
@@ -919,7 +942,7 @@ __device__ void attention_scores_body(const ScoresArgs &a, int block) {
       for (int u = 0; u < kScoreBatch; ++u) {
         int t = base + u * rowsPerLoad + sub;
         t = t < w1 ? t : min(w0 + sub, w1 - 1);    // past the end: re-read an early row, dropped
-        kv[u] = stream_load4(keys + long(t) * a.D + 4 * part);
+        kv[u] = load4<NT>(keys + long(t) * a.D + 4 * part);
       }
 #pragma unroll
       for (int u = 0; u < kScoreBatch; ++u) {
@@ -932,7 +955,8 @@ __device__ void attention_scores_body(const ScoresArgs &a, int block) {
     for (int t = t0 + threadIdx.x; t < tEnd; t += kBlock) scores[t] = score_scalar(q, keys + long(t) * a.D, a.D) * a.scale;
   }
 }
-CKL_ENTRY(attention_scores, ScoresArgs, attention_scores_body)
+CKL_ENTRY(attention_scores, ScoresArgs, attention_scores_body<false>)
+CKL_ENTRY(attention_scores_nt, ScoresArgs, attention_scores_body<true>)
 
 // ------------------------------------------------------------------ softmax
 // probs[b,h,t] = exp(s[t] - max) / sum_t' exp(s[t'] - max) over t <= p (workloads.py:114-128).
@@ -1030,6 +1054,7 @@ __device__ __forceinline__ bool values_vector_layout(int D) { return (D & 3) == 
 // A thread's kValuesBatch cache-row loads of the values' vector layout, rows base + u*groups + g
 // (rows past `end` re-read an early row; end > 0).
 struct ValueBatch { float4 v[kValuesBatch]; };
+template <bool NT>
 __device__ __forceinline__ void load_value_batch(ValueBatch &vb, const float *values, int D, int base, int end) {
   const int width = D / 4, groups = int(blockDim.x) / width;
   const int g = threadIdx.x / width, part = threadIdx.x % width;
@@ -1037,7 +1062,7 @@ __device__ __forceinline__ void load_value_batch(ValueBatch &vb, const float *va
   for (int u = 0; u < kValuesBatch; ++u) {
     int t = base + u * groups + g;
     int tc = t < end ? t : min(g, end - 1);        // past the end: re-read an early row, weight 0
-    vb.v[u] = stream_load4(values + long(tc) * D + 4 * part);
+    vb.v[u] = load4<NT>(values + long(tc) * D + 4 * part);
   }
 }
 __device__ __forceinline__ const float *values_slab(const ValuesArgs &a, long bh) {
@@ -1045,6 +1070,7 @@ __device__ __forceinline__ const float *values_slab(const ValuesArgs &a, long bh
 }
 // `haveFirst`: `first` holds this thread's first batch (vector layout, end > 0). `p` is the
 // position (a.position[0]), loaded by the caller.
+template <bool NT>
 __device__ __forceinline__ void attention_values_row(const ValuesArgs &a, long bh, const float *probs,
                                                      const ValueBatch &first, bool haveFirst, int p) {
   __shared__ float4 partial[kValuesBlock];
@@ -1076,7 +1102,7 @@ __device__ __forceinline__ void attention_values_row(const ValuesArgs &a, long b
     }
     for (; base < end; base += step) {
       ValueBatch vb;
-      load_value_batch(vb, values, a.D, base, end);
+      load_value_batch<NT>(vb, values, a.D, base, end);
       consume(vb, base);
     }
     partial[threadIdx.x] = acc;
@@ -1099,20 +1125,21 @@ __device__ __forceinline__ void attention_values_row(const ValuesArgs &a, long b
   }
 }
 
-__device__ void attention_values_body(const ValuesArgs &a, int block) {
+template <bool NT> __device__ void attention_values_body(const ValuesArgs &a, int block) {
   long bh = block;
   if (bh >= long(a.B) * a.A) return;
   ValueBatch none;
-  attention_values_row(a, bh, a.probs + bh * a.T, none, false, load_position(a.position));
+  attention_values_row<NT>(a, bh, a.probs + bh * a.T, none, false, load_position(a.position));
 }
-CKL_ENTRY_ATTR(attention_values, ValuesArgs, attention_values_body, kValuesBlock, )
+CKL_ENTRY_ATTR(attention_values, ValuesArgs, attention_values_body<false>, kValuesBlock, )
+CKL_ENTRY_ATTR(attention_values_nt, ValuesArgs, attention_values_body<true>, kValuesBlock, )
 
 // softmax -> attention_values as one launch of attention_values's geometry (one workgroup per
 // (b, h), blockDim >= rowThreads, checked by the executor): lanes [0, rowThreads) compute the
 // row's softmax exactly as the softmax kernel does, writing probs and an LDS copy of the row
 // (T <= kChainSoftmaxRow floats of dynamic shared memory), then the workgroup reduces the values
 // from the LDS copy.
-__device__ void softmax__attention_values_body(const SoftmaxValuesChainArgs &a, int block) {
+template <bool NT> __device__ void softmax__attention_values_body(const SoftmaxValuesChainArgs &a, int block) {
   extern __shared__ float rowProbs[];
   long bh = block;
   if (bh >= long(a.values.B) * a.values.A) return;
@@ -1121,9 +1148,10 @@ __device__ void softmax__attention_values_body(const SoftmaxValuesChainArgs &a, 
               int(threadIdx.x) < rowThreads, rowProbs, load_position(a.softmax.position));
   __syncthreads();
   ValueBatch none;
-  attention_values_row(a.values, bh, rowProbs, none, false, load_position(a.values.position));
+  attention_values_row<NT>(a.values, bh, rowProbs, none, false, load_position(a.values.position));
 }
-CKL_ENTRY_ATTR(softmax__attention_values, SoftmaxValuesChainArgs, softmax__attention_values_body, kValuesBlock, )
+CKL_ENTRY_ATTR(softmax__attention_values, SoftmaxValuesChainArgs, softmax__attention_values_body<false>, kValuesBlock, )
+CKL_ENTRY_ATTR(softmax__attention_values_nt, SoftmaxValuesChainArgs, softmax__attention_values_body<true>, kValuesBlock, )
 
 // attention_scores -> softmax -> attention_values as one launch of attention_values's geometry
 // (one workgroup per (b, h)): the workgroup computes the row's scores into LDS (the waves stride
@@ -1142,13 +1170,14 @@ struct KeyLayout {
     part = lane % width;
   }
 };
+template <bool NT>
 __device__ __forceinline__ void load_key_batch(KeyBatch &kb, const float *keys, int D, const KeyLayout &k, int base,
                                                int end) {
 #pragma unroll
   for (int u = 0; u < kScoreBatch; ++u) {
     int t = base + u * k.rowsPerLoad + k.sub;
     t = t < end ? t : min(k.sub, end - 1);        // past the end: re-read an early row, dropped
-    kb.kv[u] = stream_load4(keys + long(t) * D + 4 * k.part);
+    kb.kv[u] = load4<NT>(keys + long(t) * D + 4 * k.part);
   }
 }
 __device__ __forceinline__ void score_key_batch(const KeyBatch &kb, float4 qv, const KeyLayout &k, int base, int end,
@@ -1170,6 +1199,7 @@ __device__ __forceinline__ void score_key_batch(const KeyBatch &kb, float4 qv, c
 // `appended` (the rope chain, position in range), the key row at the position is read from LDS
 // instead of the cache and `storesPending` waves wait for their cache-row stores before the
 // barrier that precedes the values. The first batch of value rows is loaded before the softmax.
+template <bool NT>
 __device__ __forceinline__ void attention_chain_row(const ScoresArgs &sc, const SoftmaxArgs &softmax,
                                                     const ValuesArgs &values, long bh, const float *q,
                                                     float *rowScores, const KeyBatch &first, bool haveFirst,
@@ -1193,7 +1223,7 @@ __device__ __forceinline__ void attention_chain_row(const ScoresArgs &sc, const 
     }
     for (; base < endG; base += step) {
       KeyBatch kb;
-      load_key_batch(kb, keys, sc.D, k, base, endG);
+      load_key_batch<NT>(kb, keys, sc.D, k, base, endG);
       score_key_batch(kb, qv, k, base, endG, sc.scale, rowScores, scores);
     }
     if (appended && wave == 0) {
@@ -1216,22 +1246,25 @@ __device__ __forceinline__ void attention_chain_row(const ScoresArgs &sc, const 
   __syncthreads();
   ValueBatch vfirst;
   const bool haveV = values_vector_layout(values.D) && end > 0;
-  if (haveV) load_value_batch(vfirst, values_slab(values, bh), values.D, 0, end);
+  if (haveV) load_value_batch<NT>(vfirst, values_slab(values, bh), values.D, 0, end);
   const int rowThreads = softmax.rowThreads;
   softmax_row(softmax, rowScores, bh, int(threadIdx.x) % rowThreads, int(threadIdx.x) < rowThreads, rowScores, p);
   __syncthreads();
-  attention_values_row(values, bh, rowScores, vfirst, haveV, p);
+  attention_values_row<NT>(values, bh, rowScores, vfirst, haveV, p);
 }
 
+template <bool NT>
 __device__ void attention_scores__softmax__attention_values_body(const AttentionChainArgs &a, int block) {
   extern __shared__ float rowScores[];
   long bh = block;
   if (bh >= long(a.values.B) * a.values.A) return;
   KeyBatch none;
-  attention_chain_row(a.scores, a.softmax, a.values, bh, a.scores.q + bh * a.scores.D, rowScores, none, false);
+  attention_chain_row<NT>(a.scores, a.softmax, a.values, bh, a.scores.q + bh * a.scores.D, rowScores, none, false);
 }
 CKL_ENTRY_ATTR(attention_scores__softmax__attention_values, AttentionChainArgs,
-               attention_scores__softmax__attention_values_body, kValuesBlock, )
+               attention_scores__softmax__attention_values_body<false>, kValuesBlock, )
+CKL_ENTRY_ATTR(attention_scores__softmax__attention_values_nt, AttentionChainArgs,
+               attention_scores__softmax__attention_values_body<true>, kValuesBlock, )
 
 // rope(q), rope(k) -> append_kv -> attention_scores -> softmax -> attention_values as one launch
 // of attention_values's geometry: workgroup (b, h) first rotates its head's pairs of q and k at
@@ -1243,8 +1276,8 @@ CKL_ENTRY_ATTR(attention_scores__softmax__attention_values, AttentionChainArgs,
 // [0, T) only if the caller lets it run past the cache capacity; then rope and append write
 // nothing and the attention reads q's buffer, as the separate dispatches would.
 // Dynamic LDS: the row of T scores (padded to 4 floats), then the D-float query and key rows.
-__device__ void rope__rope__append_kv__attention_scores__softmax__attention_values_body(
-    const RopeAttentionChainArgs &a, int block) {
+template <bool NT>
+__device__ void rope_attention_stream(const RopeAttentionChainArgs &a, int block) {
   extern __shared__ float rowScores[];
   const RopeArgs &q = a.q, &k = a.k;
   const AppendArgs &ap = a.append;
@@ -1264,7 +1297,8 @@ __device__ void rope__rope__append_kv__attention_scores__softmax__attention_valu
   const bool early = vector && inRange && p >= int(blockDim.x >> 6) * kScoreBatch * layout.rowsPerLoad;
   KeyBatch first;
   if (early)
-    load_key_batch(first, sc.kc + (long(sc.layer) * sc.B * sc.A + bh) * long(sc.T) * sc.D, sc.D, layout, firstBase, p);
+    load_key_batch<NT>(first, sc.kc + (long(sc.layer) * sc.B * sc.A + bh) * long(sc.T) * sc.D, sc.D, layout, firstBase,
+                       p);
   if (inRange) {
     for (int r = threadIdx.x; r < q.R; r += blockDim.x) {
       long c = bh * (2L * q.R) + 2 * r;              // = b*(2R*A) + h*2R + 2r
@@ -1283,11 +1317,13 @@ __device__ void rope__rope__append_kv__attention_scores__softmax__attention_valu
   __syncthreads();
   // The barrier alone does not wait for vector stores: the waves that appended cache rows wait for
   // them before the barrier that precedes the values (the scores take the key row from LDS).
-  attention_chain_row(a.scores, a.softmax, a.values, bh, inRange ? qrow : sc.q + bh * sc.D, rowScores, first,
+  attention_chain_row<NT>(a.scores, a.softmax, a.values, bh, inRange ? qrow : sc.q + bh * sc.D, rowScores, first,
                       early, inRange ? krow : nullptr, inRange && int(threadIdx.x & ~63) < q.R);
 }
 CKL_ENTRY_ATTR(rope__rope__append_kv__attention_scores__softmax__attention_values, RopeAttentionChainArgs,
-               rope__rope__append_kv__attention_scores__softmax__attention_values_body, kValuesBlock, )
+               rope_attention_stream<false>, kValuesBlock, )
+CKL_ENTRY_ATTR(rope__rope__append_kv__attention_scores__softmax__attention_values_nt, RopeAttentionChainArgs,
+               rope_attention_stream<true>, kValuesBlock, )
 
 // ------------------------------------------------------------------ pointwise
 // add: dst = x + y; multiply: dst = x * y; silu: dst = v / (1 + exp(-v)) (workloads.py:145-167).

@@ -523,7 +523,20 @@ std::vector<Chain> findChains(const Plan &plan, const std::vector<bool> &tempora
         trace(head, rule, "the code object has no such entry point");
         continue;
       }
-      std::string groupName = std::string(rule.entry) + "_group";
+      // A chain with a streaming member runs its nontemporal-load variant when there is one.
+      std::string entry = rule.entry;
+      bool streaming = false;
+      for (size_t m : roles) streaming |= streams(plan.nodes[m].launch);
+      if (streaming) {
+        hipFunction_t variant = nullptr;
+        if (hipModuleGetFunction(&variant, first.module, (entry + "_nt").c_str()) == hipSuccess) {
+          function = variant;
+          entry += "_nt";
+        } else {
+          (void)hipGetLastError();
+        }
+      }
+      std::string groupName = entry + "_group";
       if (hipModuleGetFunction(&group, first.module, groupName.c_str()) != hipSuccess) {
         (void)hipGetLastError();
         group = nullptr;
@@ -576,6 +589,24 @@ std::vector<Chain> findChains(const Plan &plan, const std::vector<bool> &tempora
     }
   }
   return chains;
+}
+
+bool streams(const Launch &l) {
+  const std::string &name = l.name;
+  if (name.rfind("ckl_linear_mfma", 0) == 0 || name == "ckl_linear_rowvec") {
+    if (l.arguments.size() != sizeof(LinearArgs)) return false;
+    const LinearArgs a = block<LinearArgs>(l);
+    return int64_t(a.I) * a.O * 4 >= kStreamBytes;
+  }
+  if (name == "ckl_attention_scores" && l.arguments.size() == sizeof(ScoresArgs)) {
+    const ScoresArgs a = block<ScoresArgs>(l);
+    return int64_t(a.B) * a.A * a.T * a.D * 4 >= kStreamBytes;
+  }
+  if (name == "ckl_attention_values" && l.arguments.size() == sizeof(ValuesArgs)) {
+    const ValuesArgs a = block<ValuesArgs>(l);
+    return int64_t(a.B) * a.A * a.T * a.D * 4 >= kStreamBytes;
+  }
+  return false;
 }
 
 bool sharesOperands(const std::vector<const Launch *> &members) {

@@ -147,6 +147,20 @@ GraphExec::~GraphExec() {
   if (graph) hipGraphDestroy(graph);
 }
 
+void bindVariants(Launch &launch, const std::string &entry) {
+  launch.groupFunction = nullptr;
+  launch.sharedFunction[0] = launch.sharedFunction[1] = nullptr;
+  hipFunction_t group = nullptr;
+  if (hipModuleGetFunction(&group, launch.module, (entry + "_group").c_str()) == hipSuccess) launch.groupFunction = group;
+  else (void)hipGetLastError();
+  for (int m = 2; m <= 3; ++m) {
+    hipFunction_t shared = nullptr;
+    std::string sharedName = entry + "_shared" + std::to_string(m);
+    if (hipModuleGetFunction(&shared, launch.module, sharedName.c_str()) == hipSuccess) launch.sharedFunction[m - 2] = shared;
+    else (void)hipGetLastError();
+  }
+}
+
 namespace {
 
 constexpr size_t kMaxGroup = 4;
@@ -675,16 +689,7 @@ extern "C" void ckl_kernel(void *frame, const char *name, uint64_t gx, uint64_t 
     launch.name = name;
     launch.module = f.module;
     ckl::rt::check(hipModuleGetFunction(&launch.function, f.module, name), "hipModuleGetFunction");
-    hipFunction_t group = nullptr;
-    std::string groupName = std::string(name) + "_group";
-    if (hipModuleGetFunction(&group, f.module, groupName.c_str()) == hipSuccess) launch.groupFunction = group;
-    else (void)hipGetLastError();
-    for (int m = 2; m <= 3; ++m) {
-      std::string sharedName = std::string(name) + "_shared" + std::to_string(m);
-      hipFunction_t shared = nullptr;
-      if (hipModuleGetFunction(&shared, f.module, sharedName.c_str()) == hipSuccess) launch.sharedFunction[m - 2] = shared;
-      else (void)hipGetLastError();
-    }
+    ckl::rt::bindVariants(launch, name);
     uint64_t dims[6] = {gx, gy, gz, bx, by, bz};
     for (uint64_t d : dims)
       if (!d || d > 0xffffffffull) throw std::invalid_argument("kernel launch dimensions must be positive 32-bit values");
@@ -728,6 +733,17 @@ extern "C" void ckl_commit(void *frame, uint64_t id) {
   ckl::rt::callback(frame, [&](Invocation &f) {
     f.pending.arguments.resize((f.pending.arguments.size() + 7) & ~size_t(7), 0);
     if (f.pending.arguments.empty()) f.pending.arguments.resize(8, 0);
+    // A library kernel whose streamed operand is large runs its nontemporal-load variant.
+    if (f.pending.module && ckl::rt::streams(f.pending)) {
+      hipFunction_t variant = nullptr;
+      std::string nt = f.pending.name + "_nt";
+      if (hipModuleGetFunction(&variant, f.pending.module, nt.c_str()) == hipSuccess) {
+        f.pending.function = variant;
+        ckl::rt::bindVariants(f.pending, nt);
+      } else {
+        (void)hipGetLastError();
+      }
+    }
     f.nodes[id] = f.plan.addKernel(std::move(f.pending), std::move(f.dependencies));
     f.pending = Launch();
     f.dependencies.clear();

@@ -98,6 +98,11 @@ std::map<size_t, Launch> deferCombines(const Plan &plan, const std::vector<bool>
 // Whether sibling launches of one entry point read the same operand the way its _shared<M> entry
 // point requires (linears multiplying the same x with one shape and tiling).
 bool sharesOperands(const std::vector<const Launch *> &members);
+// Whether a library launch streams at least kStreamBytes of weights or cache (its <entry>_nt
+// variant reads them with nontemporal loads).
+bool streams(const Launch &launch);
+// Looks up the _group and _shared<M> entry points of `entry` in the launch's module.
+void bindVariants(Launch &launch, const std::string &entry);
 
 struct GraphExec {
   hipGraph_t graph = nullptr;
