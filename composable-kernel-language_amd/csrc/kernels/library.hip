@@ -477,14 +477,16 @@ template <int J, int S, int M> struct MfmaStage {
   float w[M][2 * S][4][J];
 };
 
+// A prefetch past the wave's last full stage (`dead`, issued only to keep the loop free of
+// conditional loads) reads the workspace's zero page instead: one cache line for the wave.
 template <int J, int S, int M, bool Tail, bool NT>
 __device__ __forceinline__ void mfma_load(MfmaStage<J, S, M> &st, const float *xr, const float *const (&w)[M], long O,
-                                          int k, int k1) {
+                                          int k, int k1, bool dead = false, const float *zero = nullptr) {
 #pragma unroll
   for (int u = 0; u < 2 * S; ++u) {
     const int kk = k + 8 * u;
     if constexpr (!Tail) {
-      float4 v = *reinterpret_cast<const float4 *>(xr + kk);
+      float4 v = *reinterpret_cast<const float4 *>(dead ? zero : xr + kk);
       st.x[u][0] = v.x; st.x[u][1] = v.y; st.x[u][2] = v.z; st.x[u][3] = v.w;
     }
 #pragma unroll
@@ -502,7 +504,7 @@ __device__ __forceinline__ void mfma_load(MfmaStage<J, S, M> &st, const float *x
         }
       } else {
 #pragma unroll
-        for (int m = 0; m < M; ++m) load_columns<J, NT>(st.w[m][u][i], w[m] + long(kk + i) * O);
+        for (int m = 0; m < M; ++m) load_columns<J, NT>(st.w[m][u][i], dead ? zero : w[m] + long(kk + i) * O);
       }
     }
   }
@@ -631,7 +633,7 @@ __device__ void linear_mfma(const LinearArgs *a, int block, float *smem) {
   // Full stages are double-buffered: stage u+1's loads are in flight while stage u feeds the
   // MFMAs (S sets how many bytes each wave keeps in flight). The loop body has no conditional
   // loads (the compiler would sink them into the condition and drain the load queue at the join);
-  // with an even stage count the last prefetch re-reads the last stage, an L2 hit. sched_barrier
+  // with an even stage count the last prefetch is dead and reads the zero page. sched_barrier
   // keeps each stage's loads issued as one group ahead of the other stage's MFMAs. The ragged
   // rest of the slice is cut into 16-row tail stages, dealt round-robin after the full ones.
   constexpr int R = 16 * S;
@@ -648,7 +650,8 @@ __device__ void linear_mfma(const LinearArgs *a, int block, float *smem) {
     __builtin_amdgcn_sched_barrier(0);
     stage_compute<F, J, S, M>(sa, acc);
     __builtin_amdgcn_sched_barrier(0);
-    mfma_load<J, S, M, false, NT>(sa, xr, w, O, k + 4 * R * min(t + 2, full - 1), k1);
+    mfma_load<J, S, M, false, NT>(sa, xr, w, O, k + 4 * R * min(t + 2, full - 1), k1, t + 2 >= full,
+                                  reinterpret_cast<const float *>(a0.workspace));
     __builtin_amdgcn_sched_barrier(0);
     stage_compute<F, J, S, M>(sb, acc);
     __builtin_amdgcn_sched_barrier(0);
