@@ -903,22 +903,79 @@ CKL_ENTRY(rope__rope__append_kv, RopeAppendChainArgs, rope__rope__append_kv_body
 // ------------------------------------------------------------------ attention_scores
 // scores[b,h,t] = (sum_d q[b,h*D+d] * kc[layer,b,h,t,d]) * scale for t <= p (workloads.py:100-111).
 // One 256-thread workgroup per (b, h, 256-row chunk); each wave owns 64 consecutive cache rows.
-// Groups of D/4 lanes hold one row as float4s; a wave issues kScoreBatch row loads per lane before
+// Rows are held in the vector layout below; a wave issues kScoreBatch float4 loads per lane before
 // reducing any of them, so ~kScoreBatch KB per wave are in flight. Row addresses past the end
 // re-read an early row of the wave and their results are dropped (the loads stay unpredicated).
+// The row arithmetic is shared with the attention chains; rows the vector layout does not cover
+// use the sequential dot product.
 constexpr int kScoreBatch = 8;
-// Row arithmetic shared by attention_scores and its chain: a lane's 4-element partial dot
-// product (explicit FMAs), summed over the row's D/4 lanes by group_sum; rows the vector layout
-// does not cover use the sequential dot product.
-__device__ __forceinline__ float dot4(float4 q, float4 k) {
-  return __builtin_fmaf(q.w, k.w, __builtin_fmaf(q.z, k.z, __builtin_fmaf(q.y, k.y, q.x * k.x)));
-}
 __device__ __forceinline__ float score_scalar(const float *q, const float *key, int D) {
   float v = 0.f;
   for (int d = 0; d < D; ++d) v = __builtin_fmaf(q[d], key[d], v);
   return v;
 }
-__device__ __forceinline__ bool scores_vector_layout(int D) { return (D & 3) == 0 && D <= 256 && (64 % (D / 4)) == 0; }
+// Vector layout of the scores: groups of G lanes hold one cache row, each lane P float4 pieces of
+// it (pieces part + G*j, j < P): P = 1 and G = D/4 for D <= 32, else G = 8 lanes (G = 16 for
+// D = 256) and P = D/32 (at most 4). Each lane adds its 4P products with explicit FMAs in piece
+// order, then the row is summed over its G lanes (group_sum), so with 8-lane groups a row costs
+// three DPP steps instead of a 32-lane butterfly. A wave load covers 64/G rows; a lane keeps
+// kScoreBatch pieces in flight (kScoreBatch/P rows).
+__device__ __forceinline__ bool scores_vector_layout(int D) {
+  if ((D & 3) || D > 256) return false;
+  return D <= 32 ? (64 % (D / 4)) == 0 : (D % 32) == 0;
+}
+__device__ __forceinline__ int score_pieces(int D) { return D <= 32 ? 1 : min(D / 32, 4); }
+// Partial dot product of a lane's P pieces of q and of one key row.
+template <int P> __device__ __forceinline__ float dot_pieces(const float4 (&q)[P], const float4 *k) {
+  float v = q[0].x * k[0].x;
+  v = __builtin_fmaf(q[0].y, k[0].y, v);
+  v = __builtin_fmaf(q[0].z, k[0].z, v);
+  v = __builtin_fmaf(q[0].w, k[0].w, v);
+#pragma unroll
+  for (int j = 1; j < P; ++j) {
+    v = __builtin_fmaf(q[j].x, k[j].x, v);
+    v = __builtin_fmaf(q[j].y, k[j].y, v);
+    v = __builtin_fmaf(q[j].z, k[j].z, v);
+    v = __builtin_fmaf(q[j].w, k[j].w, v);
+  }
+  return v;
+}
+template <int P> struct KeyLayout {
+  static constexpr int U = kScoreBatch / P;        // rows per lane per batch
+  int G, rowsPerLoad, sub, part;
+  __device__ explicit KeyLayout(int D) : G(D / (4 * P)), rowsPerLoad(64 / (D / (4 * P))) {
+    const int lane = threadIdx.x & 63;
+    sub = lane / G;
+    part = lane % G;
+  }
+  __device__ int rowsPerBatch() const { return U * rowsPerLoad; }
+  template <typename T> __device__ void loadQuery(float4 (&qv)[P], const T *q) const {
+#pragma unroll
+    for (int j = 0; j < P; ++j) qv[j] = reinterpret_cast<const float4 *>(q)[part + G * j];
+  }
+};
+template <bool NT, int P> __device__ void attention_scores_rows(const ScoresArgs &a, const float *q, const float *keys,
+                                                          float *scores, int w0, int w1) {
+  const KeyLayout<P> k(a.D);
+  float4 qv[P];
+  k.loadQuery(qv, q);
+  for (int base = w0; base < w1; base += k.rowsPerBatch()) {
+    float4 kv[kScoreBatch];
+#pragma unroll
+    for (int u = 0; u < k.U; ++u) {
+      int t = base + u * k.rowsPerLoad + k.sub;
+      t = t < w1 ? t : min(w0 + k.sub, w1 - 1);    // past the end: re-read an early row, dropped
+#pragma unroll
+      for (int j = 0; j < P; ++j) kv[u * P + j] = load4<NT>(keys + long(t) * a.D + 4 * (k.part + k.G * j));
+    }
+#pragma unroll
+    for (int u = 0; u < k.U; ++u) {
+      float v = group_sum(dot_pieces<P>(qv, kv + u * P), k.G);
+      int t = base + u * k.rowsPerLoad + k.sub;
+      if (k.part == 0 && t < w1) scores[t] = v * a.scale;
+    }
+  }
+}
 template <bool NT> __device__ void attention_scores_body(const ScoresArgs &a, int block) {
   int chunks = (a.T + kBlock - 1) / kBlock;
   int chunk = block % chunks;
@@ -933,26 +990,12 @@ template <bool NT> __device__ void attention_scores_body(const ScoresArgs &a, in
   float *scores = a.scores + bh * a.T;
   int tEnd = min(t0 + kBlock, end);
   if (scores_vector_layout(a.D)) {
-    const int width = a.D / 4;                   // lanes per row
-    const int rowsPerLoad = 64 / width;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int sub = lane / width, part = lane % width;
-    const float4 qv = reinterpret_cast<const float4 *>(q)[part];
+    const int wave = threadIdx.x >> 6;
     const int w0 = t0 + wave * 64, w1 = min(w0 + 64, tEnd);
-    for (int base = w0; base < w1; base += kScoreBatch * rowsPerLoad) {
-      float4 kv[kScoreBatch];
-#pragma unroll
-      for (int u = 0; u < kScoreBatch; ++u) {
-        int t = base + u * rowsPerLoad + sub;
-        t = t < w1 ? t : min(w0 + sub, w1 - 1);    // past the end: re-read an early row, dropped
-        kv[u] = load4<NT>(keys + long(t) * a.D + 4 * part);
-      }
-#pragma unroll
-      for (int u = 0; u < kScoreBatch; ++u) {
-        float v = group_sum(dot4(qv, kv[u]), width);
-        int t = base + u * rowsPerLoad + sub;
-        if (part == 0 && t < w1) scores[t] = v * a.scale;
-      }
+    switch (score_pieces(a.D)) {
+      case 1: attention_scores_rows<NT, 1>(a, q, keys, scores, w0, w1); break;
+      case 2: attention_scores_rows<NT, 2>(a, q, keys, scores, w0, w1); break;
+      default: attention_scores_rows<NT, 4>(a, q, keys, scores, w0, w1); break;
     }
   } else {
     for (int t = t0 + threadIdx.x; t < tEnd; t += kBlock) scores[t] = score_scalar(q, keys + long(t) * a.D, a.D) * a.scale;
@@ -1164,30 +1207,26 @@ CKL_ENTRY_ATTR(softmax__attention_values_nt, SoftmaxValuesChainArgs, softmax__at
 // (only the chain reads them).
 // A wave's kScoreBatch cache-row loads of the scores' vector layout (groups of D/4 lanes hold one
 // row as float4s): rows base + u*rowsPerLoad + sub; rows past `end` re-read an early row.
+// A wave's batch of cache-row loads in the scores' vector layout (KeyLayout<P>): rows
+// base + u*rowsPerLoad + sub for u < U, P pieces each; rows past `end` re-read an early row.
 struct KeyBatch { float4 kv[kScoreBatch]; };
-struct KeyLayout {
-  int width, rowsPerLoad, sub, part;
-  __device__ explicit KeyLayout(int D) : width(D / 4), rowsPerLoad(64 / (D / 4)) {
-    const int lane = threadIdx.x & 63;
-    sub = lane / width;
-    part = lane % width;
-  }
-};
-template <bool NT>
-__device__ __forceinline__ void load_key_batch(KeyBatch &kb, const float *keys, int D, const KeyLayout &k, int base,
+template <bool NT, int P>
+__device__ __forceinline__ void load_key_batch(KeyBatch &kb, const float *keys, int D, const KeyLayout<P> &k, int base,
                                                int end) {
 #pragma unroll
-  for (int u = 0; u < kScoreBatch; ++u) {
+  for (int u = 0; u < k.U; ++u) {
     int t = base + u * k.rowsPerLoad + k.sub;
     t = t < end ? t : min(k.sub, end - 1);        // past the end: re-read an early row, dropped
-    kb.kv[u] = load4<NT>(keys + long(t) * D + 4 * k.part);
+#pragma unroll
+    for (int j = 0; j < P; ++j) kb.kv[u * P + j] = load4<NT>(keys + long(t) * D + 4 * (k.part + k.G * j));
   }
 }
-__device__ __forceinline__ void score_key_batch(const KeyBatch &kb, float4 qv, const KeyLayout &k, int base, int end,
-                                                float scale, float *rowScores, float *scores) {
+template <int P>
+__device__ __forceinline__ void score_key_batch(const KeyBatch &kb, const float4 (&qv)[P], const KeyLayout<P> &k, int base,
+                                                int end, float scale, float *rowScores, float *scores) {
 #pragma unroll
-  for (int u = 0; u < kScoreBatch; ++u) {
-    float v = group_sum(dot4(qv, kb.kv[u]), k.width) * scale;
+  for (int u = 0; u < k.U; ++u) {
+    float v = group_sum(dot_pieces<P>(qv, kb.kv + u * P), k.G) * scale;
     int t = base + u * k.rowsPerLoad + k.sub;
     if (k.part == 0 && t < end) {
       rowScores[t] = v;
@@ -1202,7 +1241,7 @@ __device__ __forceinline__ void score_key_batch(const KeyBatch &kb, float4 qv, c
 // `appended` (the rope chain, position in range), the key row at the position is read from LDS
 // instead of the cache and `storesPending` waves wait for their cache-row stores before the
 // barrier that precedes the values. The first batch of value rows is loaded before the softmax.
-template <bool NT>
+template <bool NT, int P>
 __device__ __forceinline__ void attention_chain_row(const ScoresArgs &sc, const SoftmaxArgs &softmax,
                                                     const ValuesArgs &values, long bh, const float *q,
                                                     float *rowScores, const KeyBatch &first, bool haveFirst,
@@ -1214,25 +1253,27 @@ __device__ __forceinline__ void attention_chain_row(const ScoresArgs &sc, const 
   float *scores = sc.scores ? sc.scores + bh * sc.T : nullptr;
   const bool vector = scores_vector_layout(sc.D);
   if (vector) {
-    const KeyLayout k(sc.D);
+    const KeyLayout<P> k(sc.D);
     const int wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
-    const float4 qv = reinterpret_cast<const float4 *>(q)[k.part];
-    const int step = waves * kScoreBatch * k.rowsPerLoad;
+    float4 qv[P];
+    k.loadQuery(qv, q);
+    const int step = waves * k.rowsPerBatch();
     const int endG = appended ? end - 1 : end;       // the appended row comes from LDS
-    int base = wave * kScoreBatch * k.rowsPerLoad;
+    int base = wave * k.rowsPerBatch();
     if (haveFirst) {
       score_key_batch(first, qv, k, base, endG, sc.scale, rowScores, scores);
       base += step;
     }
     for (; base < endG; base += step) {
       KeyBatch kb;
-      load_key_batch<NT>(kb, keys, sc.D, k, base, endG);
+      load_key_batch<NT, P>(kb, keys, sc.D, k, base, endG);
       score_key_batch(kb, qv, k, base, endG, sc.scale, rowScores, scores);
     }
     if (appended && wave == 0) {
       // The row's score with the arithmetic of the cache path (any lane group reduces alike).
-      const float4 kv = reinterpret_cast<const float4 *>(appended)[k.part];
-      float v = group_sum(dot4(qv, kv), k.width) * sc.scale;
+      float4 kv[P];
+      k.loadQuery(kv, appended);
+      float v = group_sum(dot_pieces<P>(qv, kv), k.G) * sc.scale;
       if ((threadIdx.x & 63) == 0) {
         rowScores[p] = v;
         if (scores) scores[p] = v;
@@ -1262,7 +1303,12 @@ __device__ void attention_scores__softmax__attention_values_body(const Attention
   long bh = block;
   if (bh >= long(a.values.B) * a.values.A) return;
   KeyBatch none;
-  attention_chain_row<NT>(a.scores, a.softmax, a.values, bh, a.scores.q + bh * a.scores.D, rowScores, none, false);
+  const float *q = a.scores.q + bh * a.scores.D;
+  switch (score_pieces(a.scores.D)) {
+    case 1: attention_chain_row<NT, 1>(a.scores, a.softmax, a.values, bh, q, rowScores, none, false); break;
+    case 2: attention_chain_row<NT, 2>(a.scores, a.softmax, a.values, bh, q, rowScores, none, false); break;
+    default: attention_chain_row<NT, 4>(a.scores, a.softmax, a.values, bh, q, rowScores, none, false); break;
+  }
 }
 CKL_ENTRY_ATTR(attention_scores__softmax__attention_values, AttentionChainArgs,
                attention_scores__softmax__attention_values_body<false>, kValuesBlock, )
@@ -1279,8 +1325,8 @@ CKL_ENTRY_ATTR(attention_scores__softmax__attention_values_nt, AttentionChainArg
 // [0, T) only if the caller lets it run past the cache capacity; then rope and append write
 // nothing and the attention reads q's buffer, as the separate dispatches would.
 // Dynamic LDS: the row of T scores (padded to 4 floats), then the D-float query and key rows.
-template <bool NT>
-__device__ void rope_attention_stream(const RopeAttentionChainArgs &a, int block) {
+template <bool NT, int P>
+__device__ void rope_attention_rows(const RopeAttentionChainArgs &a, int block) {
   extern __shared__ float rowScores[];
   const RopeArgs &q = a.q, &k = a.k;
   const AppendArgs &ap = a.append;
@@ -1295,13 +1341,13 @@ __device__ void rope_attention_stream(const RopeAttentionChainArgs &a, int block
   // loads are issued before the rotation and overlap it (the rows are not written here).
   const int wave = threadIdx.x >> 6;
   const bool vector = scores_vector_layout(sc.D);
-  const KeyLayout layout(vector ? sc.D : 4);
-  const int firstBase = wave * kScoreBatch * layout.rowsPerLoad;
-  const bool early = vector && inRange && p >= int(blockDim.x >> 6) * kScoreBatch * layout.rowsPerLoad;
+  const KeyLayout<P> layout(vector ? sc.D : 4 * P);
+  const int firstBase = wave * layout.rowsPerBatch();
+  const bool early = vector && inRange && p >= int(blockDim.x >> 6) * layout.rowsPerBatch();
   KeyBatch first;
   if (early)
-    load_key_batch<NT>(first, sc.kc + (long(sc.layer) * sc.B * sc.A + bh) * long(sc.T) * sc.D, sc.D, layout, firstBase,
-                       p);
+    load_key_batch<NT, P>(first, sc.kc + (long(sc.layer) * sc.B * sc.A + bh) * long(sc.T) * sc.D, sc.D, layout,
+                          firstBase, p);
   if (inRange) {
     for (int r = threadIdx.x; r < q.R; r += blockDim.x) {
       long c = bh * (2L * q.R) + 2 * r;              // = b*(2R*A) + h*2R + 2r
@@ -1320,8 +1366,15 @@ __device__ void rope_attention_stream(const RopeAttentionChainArgs &a, int block
   __syncthreads();
   // The barrier alone does not wait for vector stores: the waves that appended cache rows wait for
   // them before the barrier that precedes the values (the scores take the key row from LDS).
-  attention_chain_row<NT>(a.scores, a.softmax, a.values, bh, inRange ? qrow : sc.q + bh * sc.D, rowScores, first,
-                      early, inRange ? krow : nullptr, inRange && int(threadIdx.x & ~63) < q.R);
+  attention_chain_row<NT, P>(a.scores, a.softmax, a.values, bh, inRange ? qrow : sc.q + bh * sc.D, rowScores, first,
+                             early, inRange ? krow : nullptr, inRange && int(threadIdx.x & ~63) < q.R);
+}
+template <bool NT> __device__ void rope_attention_stream(const RopeAttentionChainArgs &a, int block) {
+  switch (score_pieces(a.scores.D)) {
+    case 1: rope_attention_rows<NT, 1>(a, block); break;
+    case 2: rope_attention_rows<NT, 2>(a, block); break;
+    default: rope_attention_rows<NT, 4>(a, block); break;
+  }
 }
 CKL_ENTRY_ATTR(rope__rope__append_kv__attention_scores__softmax__attention_values, RopeAttentionChainArgs,
                rope_attention_stream<false>, kValuesBlock, )
