@@ -181,11 +181,12 @@ def measured_traffic(config, family):
 
 
 def unit_family(name):
-    """Kernel family of an inferred-step launch: the library family of a plain or grouped
-    dispatch ("ckl_linear_mfma1x1_group" -> "linear"), or the chain entry point itself."""
+    """Kernel family of an inferred-step launch: the library family of a plain, grouped or
+    shared-operand dispatch ("ckl_linear_mfma1x1_group" -> "linear"), or the chain entry point
+    itself (chain entry points join their members' names with "__")."""
     name = name[len("ckl_"):] if name.startswith("ckl_") else name
     name = name[:-len("_group")] if name.endswith("_group") else name
-    return "linear" if name.startswith("linear_") else name
+    return "linear" if name.startswith("linear_") and "__" not in name else name
 
 
 def kernel_roofline(session, c, samples=7):
@@ -212,7 +213,9 @@ def kernel_roofline(session, c, samples=7):
                "silu__multiply": 8 * b * f,                                        # activation
                "rope__rope__append_kv": 8 * b * h,                                 # rotated k
                # rotated k, the attention's read of the rotated q, scores, probs
-               "rope__rope__append_kv__attention_scores__softmax__attention_values": 12 * b * h + 16 * b * a * rows}
+               "rope__rope__append_kv__attention_scores__softmax__attention_values": 12 * b * h + 16 * b * a * rows,
+               "linear_rowvec__add__rms_stats__rms_apply": 8 * b * h,                 # linear output
+               "linear_rowvec__linear_rowvec__silu__multiply": 24 * b * f}            # gate, up, activation
     per_kernel = {}
     for index, (name, members) in enumerate(units):
         families = {nodes[m][0] for m in members}

@@ -93,6 +93,13 @@ struct CKL_ALIGN SoftmaxValuesChainArgs { SoftmaxArgs softmax; ValuesArgs values
 struct CKL_ALIGN AttentionChainArgs { ScoresArgs scores; SoftmaxArgs softmax; ValuesArgs values; };
 struct CKL_ALIGN RopeAppendChainArgs { RopeArgs q; RopeArgs k; AppendArgs append; PartialSource qsrc, ksrc, v; };
 struct CKL_ALIGN GreedyAdvanceChainArgs { GreedyArgs greedy; AdvanceArgs advance; };
+// Row-parallel linear (one tile, one slice: a workgroup owns a whole output row) -> add ->
+// rms_stats -> rms_apply; linearIsY: the linear's output is add's y operand.
+struct CKL_ALIGN LinearAddRmsChainArgs {
+  LinearArgs linear; BinaryArgs add; RmsStatsArgs stats; RmsApplyArgs apply; int linearIsY, pad;
+};
+// Two row-parallel linears of one x (gate, up; one slice) -> silu(gate) -> multiply by up.
+struct CKL_ALIGN LinearSiluChainArgs { LinearArgs gate; LinearArgs up; UnaryArgs silu; BinaryArgs multiply; };
 // rope(q), rope(k) -> append_kv -> attention_scores -> softmax -> attention_values per (b, h).
 struct CKL_ALIGN RopeAttentionChainArgs {
   RopeArgs q; RopeArgs k; AppendArgs append; ScoresArgs scores; SoftmaxArgs softmax; ValuesArgs values;

@@ -731,13 +731,12 @@ __device__ void linear_mfma(const LinearArgs *a, int block, float *smem) {
 // across workgroups.
 constexpr int kVectorRows = 64;
 constexpr int kVectorWaves = 16;
-template <bool NT> __device__ void linear_rowvec_stream(const LinearArgs &a, int block) {
-  __shared__ float red[kVectorWaves][64];
+// This wave's partial sum for output column tn*64 + lane of batch row b over its kVectorRows
+// reduction rows of slice kg (the caller combines the waves in wave order).
+template <bool NT> __device__ __forceinline__ float rowvec_partial(const LinearArgs &a, int b, int tn, int kg) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int waves = blockDim.x >> 6;
-  const int tn = block % a.tilesN, rest = block / a.tilesN;
-  const int b = rest % a.B, kg = rest / a.B;
   const int col = tn * 64 + lane;
   const bool colOk = col < a.O;
   const int span = waves * kVectorRows;
@@ -760,7 +759,19 @@ template <bool NT> __device__ void linear_rowvec_stream(const LinearArgs &a, int
 #pragma unroll
     for (int u = 0; u < kVectorRows; ++u) acc += (k0 + u < k1 ? xr[min(k0 + u, k1 - 1)] : 0.f) * wv[u];
   }
-  red[wave][lane] = acc;
+  return acc;
+}
+
+template <bool NT> __device__ void linear_rowvec_stream(const LinearArgs &a, int block) {
+  __shared__ float red[kVectorWaves][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int waves = blockDim.x >> 6;
+  const int tn = block % a.tilesN, rest = block / a.tilesN;
+  const int b = rest % a.B, kg = rest / a.B;
+  const int col = tn * 64 + lane;
+  const bool colOk = col < a.O;
+  red[wave][lane] = rowvec_partial<NT>(a, b, tn, kg);
   __syncthreads();
   if (wave != 0 || !colOk) {
     if (a.kSplit == 1 || a.deferred) return;
@@ -1435,6 +1446,95 @@ __device__ void silu__multiply_body(const SiluMultiplyChainArgs &a, int block) {
   }
 }
 CKL_ENTRY(silu__multiply, SiluMultiplyChainArgs, silu__multiply_body)
+
+
+// Row-parallel linear chains. With one column tile (O <= 64) and one slice a rowvec workgroup
+// holds a whole output row, so the row ops after the linear run in the same workgroup: linear ->
+// add -> rms_stats -> rms_apply (the o and down projections of a narrow decoder), and, for any O
+// and one slice, the two linears of one x -> silu -> multiply (gate/up). The linear columns are
+// computed and combined exactly as linear_rowvec does. For the rms, C <= 64 keeps every value of
+// the row in wave 0, the only wave with data in the 256-thread rms kernels, and the sums follow
+// their order (float4 t or element t per thread, the wave sum, then the block sum's zeros).
+template <bool NT> __device__ void linear_add_rms_stream(const LinearAddRmsChainArgs &a, int block) {
+  __shared__ float red[kVectorWaves][64];
+  __shared__ float4 row4[16];
+  const LinearArgs &l = a.linear;
+  const int b = block;
+  if (b >= l.B) return;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int waves = blockDim.x >> 6;
+  const int C = a.stats.C;
+  float *rowf = reinterpret_cast<float *>(row4);
+  red[wave][lane] = rowvec_partial<NT>(l, b, 0, 0);
+  __syncthreads();
+  if (wave != 0) return;
+  const long base = long(b) * C;
+  if (lane < C) {
+    float v = red[0][lane];
+    for (int v2 = 1; v2 < waves; ++v2) v += red[v2][lane];
+    if (l.dst) l.dst[long(b) * l.O + lane] = v;      // null: only add reads it
+    const float other = (a.linearIsY ? a.add.x : a.add.y)[base + lane];
+    const float h = a.linearIsY ? binary<0>(other, v) : binary<0>(v, other);
+    a.add.dst[base + lane] = h;
+    rowf[lane] = h;
+  }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const bool vec = (C & 3) == 0;
+  float4 h4 = make_float4(0.f, 0.f, 0.f, 0.f);
+  float h1 = 0.f, total = 0.f;
+  if (vec) {
+    if (lane < C / 4) {
+      h4 = row4[lane];
+      total = add_squares(total, h4);
+    }
+  } else if (lane < C) {
+    h1 = rowf[lane];
+    total = __builtin_fmaf(h1, h1, total);
+  }
+  total = wave_sum(total);
+  total = (total + 0.f) + (0.f + 0.f);               // block_sum over four waves, three of them empty
+  const float s = rms_inverse(total, C, a.stats.eps);
+  if (lane == 0 && a.stats.inv) a.stats.inv[b] = s;  // null: only the chain reads inv
+  const float *gain = a.apply.gain + long(a.apply.layer) * C;
+  if (vec) {
+    if (lane < C / 4)
+      reinterpret_cast<float4 *>(a.apply.dst + base)[lane] =
+          rms_scale(h4, s, reinterpret_cast<const float4 *>(gain)[lane]);
+  } else if (lane < C) {
+    a.apply.dst[base + lane] = h1 * s * gain[lane];
+  }
+}
+CKL_ENTRY_ATTR(linear_rowvec__add__rms_stats__rms_apply, LinearAddRmsChainArgs, linear_add_rms_stream<false>, 1024, )
+CKL_ENTRY_ATTR(linear_rowvec__add__rms_stats__rms_apply_nt, LinearAddRmsChainArgs, linear_add_rms_stream<true>, 1024, )
+
+template <bool NT> __device__ void linear_silu_stream(const LinearSiluChainArgs &a, int block) {
+  __shared__ float red[2][kVectorWaves][64];
+  const LinearArgs &g = a.gate, &u = a.up;
+  const int tn = block % g.tilesN, b = block / g.tilesN;
+  if (b >= g.B) return;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int waves = blockDim.x >> 6;
+  red[0][wave][lane] = rowvec_partial<NT>(g, b, tn, 0);
+  red[1][wave][lane] = rowvec_partial<NT>(u, b, tn, 0);
+  __syncthreads();
+  const int col = tn * 64 + lane;
+  if (wave != 0 || col >= g.O) return;
+  float gv = red[0][0][lane], uv = red[1][0][lane];
+  for (int v2 = 1; v2 < waves; ++v2) gv += red[0][v2][lane];
+  for (int v2 = 1; v2 < waves; ++v2) uv += red[1][v2][lane];
+  const long i = long(b) * g.O + col;
+  if (g.dst) g.dst[i] = gv;                          // null: only the chain reads them
+  if (u.dst) u.dst[i] = uv;
+  const float act = silu(gv);
+  if (a.silu.dst) a.silu.dst[i] = act;
+  a.multiply.dst[i] = binary<1>(act, uv);
+}
+CKL_ENTRY_ATTR(linear_rowvec__linear_rowvec__silu__multiply, LinearSiluChainArgs, linear_silu_stream<false>, 1024, )
+CKL_ENTRY_ATTR(linear_rowvec__linear_rowvec__silu__multiply_nt, LinearSiluChainArgs, linear_silu_stream<true>, 1024, )
 
 // ------------------------------------------------------------------ greedy
 // tokens[b] = history[p, b] = first index of the maximum logit (strict '>' scan from index 0,

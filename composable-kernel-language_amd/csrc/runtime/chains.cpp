@@ -6,7 +6,8 @@
 // grid: rms_stats -> rms_apply, add -> rms_stats -> rms_apply, embedding -> rms_stats ->
 // rms_apply, silu -> multiply, rope(q), rope(k) -> append_kv -> attention_scores -> softmax ->
 // attention_values (or the rope part alone, attention_scores -> softmax -> attention_values, or
-// softmax -> attention_values) and greedy -> advance. The plan itself (nodes, edges,
+// softmax -> attention_values), greedy -> advance, and for row-parallel linears whose workgroups
+// hold whole rows, linear -> add -> rms_stats -> rms_apply and linear, linear -> silu -> multiply. The plan itself (nodes, edges,
 // argument blocks) is unchanged; only the inferred lowering contracts a chain into one unit.
 //
 // A chain is taken only when
@@ -325,6 +326,78 @@ const char *ropeAttentionChain(const Members &m, const Internal &internal, Launc
   return nullptr;
 }
 
+// Row-parallel linear whose workgroup holds a whole output row (one tile, one slice) -> add ->
+// rms_stats -> rms_apply: one workgroup per batch row.
+const char *linearAddRmsChain(const Members &m, const Internal &internal, Launch &out) {
+  LinearAddRmsChainArgs c{block<LinearArgs>(*m[0]), block<BinaryArgs>(*m[1]), block<RmsStatsArgs>(*m[2]),
+                          block<RmsApplyArgs>(*m[3]), 0, 0};
+  const LinearArgs &l = c.linear;
+  const BinaryArgs &ad = c.add;
+  const Launch &lin = *m[0];
+  if (l.tilesN != 1 || l.kSplit != 1 || l.O > 64 || l.B <= 0 || l.I <= 0 || !l.workspace)
+    return "the linear's output rows are not one workgroup's";
+  if (lin.grid[0] != unsigned(l.B) || lin.block[0] > 1024) return "the linear does not run one workgroup per row";
+  if (ad.x == ad.y) return "add takes one operand twice";
+  if (ad.x == l.dst) c.linearIsY = 0;
+  else if (ad.y == l.dst) c.linearIsY = 1;
+  else return "add does not take the linear's output";
+  if (int64_t(ad.n) != int64_t(l.B) * l.O) return "add does not cover the linear's rows";
+  std::vector<Range> ranges;
+  if (const char *why = rmsTail(c.stats, c.apply, 2, internal, ranges)) return why;
+  if (ad.dst != c.stats.x || c.stats.C != l.O || c.stats.B != l.B) return "add does not produce rms_stats's rows";
+  const uint64_t count = uint64_t(l.B), row = 4ull * uint64_t(l.O);
+  const uint64_t matrix = 4ull * uint64_t(l.I) * uint64_t(l.O);
+  if (internal(0, l.dst)) c.linear.dst = nullptr;
+  ranges.push_back(rows(l.x, count, 4ull * uint64_t(l.I), false));
+  ranges.push_back(whole(l.w + int64_t(l.layer) * l.I * l.O, matrix));
+  ranges.push_back(whole(l.workspace, kLinearZeroPage));
+  ranges.push_back(rows(c.linearIsY ? ad.x : ad.y, count, row, false));
+  ranges.push_back(rows(ad.dst, count, row, true));
+  if (c.linear.dst) ranges.push_back(rows(l.dst, count, row, true));
+  if (!hazardFree(ranges)) return kOverlap;
+  out.grid[0] = unsigned(l.B);
+  out.block[0] = lin.block[0];
+  out.shared = 0;
+  setArguments(out, c);
+  return nullptr;
+}
+
+// Two row-parallel linears of one x (one slice each) -> silu(first) -> multiply by the second.
+const char *linearSiluChain(const Members &m, const Internal &internal, Launch &out) {
+  LinearSiluChainArgs c{block<LinearArgs>(*m[0]), block<LinearArgs>(*m[1]), block<UnaryArgs>(*m[2]),
+                        block<BinaryArgs>(*m[3])};
+  const LinearArgs &g = c.gate, &u = c.up;
+  const Launch &gl = *m[0], &ul = *m[1];
+  if (g.kSplit != 1 || u.kSplit != 1 || g.x != u.x || g.B != u.B || g.I != u.I || g.O != u.O || g.tilesN != u.tilesN ||
+      g.B <= 0 || g.O <= 0 || !g.workspace || !u.workspace)
+    return "the two linears do not share x, shape and a single slice";
+  if (gl.grid[0] != ul.grid[0] || gl.block[0] != ul.block[0] || gl.grid[0] != unsigned(g.tilesN) * unsigned(g.B))
+    return "the two linears do not share the row-parallel geometry";
+  if (c.silu.src != g.dst || c.multiply.x != c.silu.dst || c.multiply.y != u.dst)
+    return "silu and multiply do not take the two linears' outputs";
+  const int64_t n = int64_t(g.B) * g.O;
+  if (c.silu.n != n || c.multiply.n != n) return "silu or multiply does not cover the linears' outputs";
+  const uint64_t count = uint64_t(g.B), row = 4ull * uint64_t(g.O);
+  const uint64_t matrix = 4ull * uint64_t(g.I) * uint64_t(g.O);
+  if (internal(0, g.dst)) c.gate.dst = nullptr;
+  if (internal(1, u.dst)) c.up.dst = nullptr;
+  if (internal(2, c.silu.dst)) c.silu.dst = nullptr;
+  std::vector<Range> ranges{rows(g.x, count, 4ull * uint64_t(g.I), false),
+                            whole(g.w + int64_t(g.layer) * g.I * g.O, matrix),
+                            whole(u.w + int64_t(u.layer) * u.I * u.O, matrix),
+                            whole(g.workspace, kLinearZeroPage), whole(u.workspace, kLinearZeroPage),
+                            rows(c.multiply.dst, count, row, true)};
+  if (c.gate.dst) ranges.push_back(rows(g.dst, count, row, true));
+  if (c.up.dst) ranges.push_back(rows(u.dst, count, row, true));
+  if (c.silu.dst) ranges.push_back(rows(c.silu.dst, count, row, true));
+  if (!hazardFree(ranges)) return kOverlap;
+  out.grid[0] = gl.grid[0];
+  out.block[0] = gl.block[0];
+  out.shared = 0;
+  setArguments(out, c);
+  return nullptr;
+}
+
 const char *greedyAdvanceChain(const Members &m, const Internal &, Launch &out) {
   GreedyAdvanceChainArgs c{block<GreedyArgs>(*m[0]), block<AdvanceArgs>(*m[1])};
   const GreedyArgs &g = c.greedy;
@@ -406,6 +479,39 @@ std::vector<size_t> matchRopeAttention(const Plan &plan, size_t head, const Succ
   return roles;
 }
 
+// Two row-parallel linears of one x whose outputs meet in silu -> multiply: the head is the
+// linear silu reads (roles: gate, up, silu, multiply).
+std::vector<size_t> matchLinearSilu(const Plan &plan, size_t head, const Successors &successors,
+                                    const std::vector<bool> &taken) {
+  const size_t n = plan.nodes.size();
+  auto rowvec = [&](size_t k) {
+    const Launch &l = plan.nodes[k].launch;
+    return !taken[k] && l.name == "ckl_linear_rowvec" && singleGrid(l) && l.arguments.size() == sizeof(LinearArgs);
+  };
+  if (!rowvec(head)) return {};
+  const LinearArgs gate = block<LinearArgs>(plan.nodes[head].launch);
+  size_t silu = n, multiply = n;
+  for (size_t s : successors[head]) {
+    const Launch &l = plan.nodes[s].launch;
+    if (!taken[s] && l.name == "ckl_silu" && singleGrid(l) && l.arguments.size() == sizeof(UnaryArgs) &&
+        block<UnaryArgs>(l).src == gate.dst && s < silu)
+      silu = s;
+  }
+  if (silu == n) return {};
+  const void *act = block<UnaryArgs>(plan.nodes[silu].launch).dst;
+  for (size_t s : successors[silu]) {
+    const Launch &l = plan.nodes[s].launch;
+    if (!taken[s] && l.name == "ckl_multiply" && singleGrid(l) && l.arguments.size() == sizeof(BinaryArgs) &&
+        block<BinaryArgs>(l).x == act && s < multiply)
+      multiply = s;
+  }
+  if (multiply == n) return {};
+  const void *y = block<BinaryArgs>(plan.nodes[multiply].launch).y;
+  for (size_t d : plan.nodes[multiply].dependencies)
+    if (d != head && rowvec(d) && block<LinearArgs>(plan.nodes[d].launch).dst == y) return {head, d, silu, multiply};
+  return {};
+}
+
 struct Rule {
   std::vector<std::string> members;   // entry points, in role order (dependency order for a path)
   const char *entry;                  // chain entry point
@@ -421,6 +527,10 @@ const std::vector<Rule> &rules() {
        {{0, offsetof(RopeArgs, src), offsetof(RopeAttentionChainArgs, qsrc)},
         {1, offsetof(RopeArgs, src), offsetof(RopeAttentionChainArgs, ksrc)},
         {2, offsetof(AppendArgs, v), offsetof(RopeAttentionChainArgs, v)}}},
+      {{"ckl_linear_rowvec", "ckl_add", "ckl_rms_stats", "ckl_rms_apply"}, "ckl_linear_rowvec__add__rms_stats__rms_apply",
+       linearAddRmsChain},
+      {{"ckl_linear_rowvec", "ckl_linear_rowvec", "ckl_silu", "ckl_multiply"},
+       "ckl_linear_rowvec__linear_rowvec__silu__multiply", linearSiluChain, matchLinearSilu},
       {{"ckl_add", "ckl_rms_stats", "ckl_rms_apply"}, "ckl_add__rms_stats__rms_apply", addRmsChain, nullptr,
        {{0, offsetof(BinaryArgs, x), offsetof(AddRmsChainArgs, x)}, {0, offsetof(BinaryArgs, y), offsetof(AddRmsChainArgs, y)}}},
       {{"ckl_embedding", "ckl_rms_stats", "ckl_rms_apply"}, "ckl_embedding__rms_stats__rms_apply", embeddingRmsChain},

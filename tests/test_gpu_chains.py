@@ -1,5 +1,5 @@
 """Library chains in the inferred graph (csrc/runtime/chains.cpp): contracted launches leave exactly
-the state the ordinary launches leave, bit for bit, the decode step runs in 8 launches per layer
+the state the ordinary launches leave, bit for bit, the decode step runs in 5-8 launches per layer
 plus 3, and a chain whose buffers overlap in a way row-by-row execution would change runs unfused."""
 import numpy as np
 import pytest
@@ -7,6 +7,7 @@ import pytest
 import ckl
 from oracle import decoder as oracle
 from programs.decoder import rms_apply, rms_stats
+from ckl.library import linear_tiling
 from programs.decoder_config import CONFIGS, Config
 from programs.harness import MUTABLE, DecoderSession
 
@@ -22,10 +23,21 @@ SPLIT_MFMA = Config(batch=20, hidden=1024, heads=8, layers=1, ffn=1536, vocab=30
 SPLIT_VECTOR = Config(batch=5, hidden=1280, heads=10, layers=1, ffn=1536, vocab=300, context=4, steps=3)
 
 
-def chained_launches(layers):
+def whole_rows(b, i, o):
+    """Row-parallel linear whose workgroup holds whole output rows (fuses with the row ops after it)."""
+    t = linear_tiling(b, i, o)
+    return t["entry"] == "ckl_linear_rowvec" and t["tiles"] == 1 and t["split"] == 1
+
+
+def chained_launches(c):
     # embedding+rms; per layer: QKV, rope pair+append+scores+softmax+values, O, add+rms,
-    # gate/up, silu+multiply, down, add+rms; then lm head, greedy+advance.
-    return 1 + 8 * layers + 2
+    # gate/up, silu+multiply, down, add+rms (O and down fused with their add+rms, gate/up with
+    # silu+multiply, when row-parallel with one slice); then lm head, greedy+advance.
+    o = 1 if whole_rows(c.batch, c.hidden, c.hidden) else 2
+    down = 1 if whole_rows(c.batch, c.ffn, c.hidden) else 2
+    t = linear_tiling(c.batch, c.hidden, c.ffn)
+    gate_up = 1 if t["entry"] == "ckl_linear_rowvec" and t["split"] == 1 else 2
+    return 1 + (2 + o + gate_up + down) * c.layers + 2
 
 
 @pytest.mark.parametrize("config", [CONFIGS["small"], REFERENCE_SMALL, AWKWARD, ODD, SPLIT_MFMA, SPLIT_VECTOR],
@@ -37,7 +49,12 @@ def test_chained_graph_is_bit_identical_to_ordinary(device, config):
     reference = oracle.expected(initial, c, c.steps)
     for reuse, inv in session.invocations.items():
         launches = inv.launch_count(mode="graph", batch_size=1)
-        assert launches == chained_launches(c.layers)
+        if reuse:
+            # Storage reuse may alias a fused linear's x with a differently sized row it writes;
+            # such a chain runs unfused (the executor's overlap check).
+            assert chained_launches(c) <= launches <= 1 + 8 * c.layers + 2
+        else:
+            assert launches == chained_launches(c)
         if c.batch > 16:
             # q/k/v and gate/up multiply one x each: shared-operand launches of the MFMA path.
             names = [name for name, _ in inv.units()]
