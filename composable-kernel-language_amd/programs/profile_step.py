@@ -40,7 +40,7 @@ def main() -> None:
     session = DecoderSession(c, device)
     state = session.state
     state.host["position"][0] = c.context - 1
-    inv = session.invocations[True]
+    inv = session.invocations[False]   # the plan bench.py's headline "inferred" variant runs
     print(f"{args.config}: {inv.launch_count(mode='graph', batch_size=1)} launches per inferred step", flush=True)
     for _ in range(args.steps):
         state.reset(("position",))
