@@ -289,6 +289,132 @@ __device__ __forceinline__ void rms_finish_row(const RmsStatsArgs &stats, const 
   }
 }
 
+// Row chains whose row fits in registers (C % 4 == 0 and C / 4 <= kRowRegisters * 256): thread t
+// keeps its R float4 values of the row (elements t, t + 256, ..., rms_stats's order) and has the
+// gain loaded with its operands, so the scale phase needs no memory round trip. Every operand load
+// of the row is issued before the first add (unpredicated, index clamped to the row; a plane
+// source of at most kSourceBatch planes loads them all at once); stores and sums cover the
+// in-range elements only. The values are those of the loop versions above and below.
+constexpr int kRowRegisters = 4;
+template <int R, bool Planes> struct RowSource { float4 v[R][Planes ? kSourceBatch : 1]; };
+template <int R, bool Planes>
+__device__ __forceinline__ void row_source_issue(const PartialSource &src, const float *own, const long (&i)[R],
+                                                 RowSource<R, Planes> &l) {
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    if constexpr (Planes) {
+#pragma unroll
+      for (int j = 0; j < kSourceBatch; ++j)
+        l.v[r][j] = *reinterpret_cast<const float4 *>(src.partials + long(min(j, src.parts - 1)) * src.planeStride + i[r]);
+    } else {
+      l.v[r][0] = *reinterpret_cast<const float4 *>(own + i[r]);
+    }
+  }
+}
+// The planes added in g order from +0, skipping indices past the last plane (source<N>'s sums).
+template <int R, bool Planes>
+__device__ __forceinline__ float4 row_source_value(const PartialSource &src, const RowSource<R, Planes> &l, int r) {
+  if constexpr (!Planes) {
+    return l.v[r][0];
+  } else {
+    float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int j = 0; j < kSourceBatch; ++j) {
+      const bool in = j < src.parts;
+      t.x += in ? l.v[r][j].x : 0.f;
+      t.y += in ? l.v[r][j].y : 0.f;
+      t.z += in ? l.v[r][j].z : 0.f;
+      t.w += in ? l.v[r][j].w : 0.f;
+    }
+    return t;
+  }
+}
+// Stores the produced row, sums its squares, and finishes rms_stats -> rms_apply from registers.
+template <int R>
+__device__ __forceinline__ void rms_finish_registers(const RmsStatsArgs &stats, const RmsApplyArgs &apply, int row,
+                                                     float *produced, const float4 (&v)[R], const float4 (&g)[R]) {
+  const int n4 = apply.C / 4;
+  float total = 0.f;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int c = int(threadIdx.x) + r * kBlock;
+    if (c < n4) {
+      reinterpret_cast<float4 *>(produced)[c] = v[r];
+      total = add_squares(total, v[r]);
+    }
+  }
+  total = block_sum(total);
+  const float s = rms_inverse(total, stats.C, stats.eps);
+  if (threadIdx.x == 0 && stats.inv) stats.inv[row] = s;
+  float4 *dst = reinterpret_cast<float4 *>(apply.dst + long(row) * apply.C);
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int c = int(threadIdx.x) + r * kBlock;
+    if (c < n4) dst[c] = rms_scale(v[r], s, g[r]);
+  }
+}
+template <int R>
+__device__ __forceinline__ void row_gain(const RmsApplyArgs &apply, const int (&c)[R], float4 (&g)[R]) {
+  const float4 *gain = reinterpret_cast<const float4 *>(apply.gain + long(apply.layer) * apply.C);
+#pragma unroll
+  for (int r = 0; r < R; ++r) g[r] = gain[c[r]];
+}
+template <int R, bool PlanesX, bool PlanesY>
+__device__ void add_rms_registers(const AddRmsChainArgs &a, int row) {
+  const int n4 = a.stats.C / 4;
+  const long base = long(row) * a.stats.C;
+  int c[R];
+  long idx[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    c[r] = min(int(threadIdx.x) + r * kBlock, n4 - 1);
+    idx[r] = base + 4 * c[r];
+  }
+  float4 g[R], v[R];
+  row_gain<R>(a.apply, c, g);
+  RowSource<R, PlanesX> x;
+  RowSource<R, PlanesY> y;
+  row_source_issue<R, PlanesX>(a.x, a.add.x, idx, x);
+  row_source_issue<R, PlanesY>(a.y, a.add.y, idx, y);
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const float4 u = row_source_value<R, PlanesX>(a.x, x, r), w = row_source_value<R, PlanesY>(a.y, y, r);
+    v[r] = make_float4(u.x + w.x, u.y + w.y, u.z + w.z, u.w + w.w);
+  }
+  rms_finish_registers<R>(a.stats, a.apply, row, a.add.dst + base, v, g);
+}
+template <int R, bool PlanesX>
+__device__ void add_rms_registers(const AddRmsChainArgs &a, int row) {
+  if (a.y.parts > 0) add_rms_registers<R, PlanesX, true>(a, row);
+  else add_rms_registers<R, PlanesX, false>(a, row);
+}
+template <int R> __device__ void add_rms_registers(const AddRmsChainArgs &a, int row) {
+  if (a.x.parts > 0) add_rms_registers<R, true>(a, row);
+  else add_rms_registers<R, false>(a, row);
+}
+template <int R> __device__ void embedding_rms_registers(const EmbeddingRmsChainArgs &a, int row) {
+  const EmbeddingArgs &e = a.embedding;
+  const int n4 = e.C / 4;
+  int c[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) c[r] = min(int(threadIdx.x) + r * kBlock, n4 - 1);
+  float4 g[R], v[R];
+  row_gain<R>(a.apply, c, g);
+  const int token = e.tokens[row];
+  const bool valid = token >= 0 && token < e.V;
+  const float nan = __builtin_nanf("");
+  const float4 *table = reinterpret_cast<const float4 *>(e.table + long(valid ? token : 0) * e.C);
+#pragma unroll
+  for (int r = 0; r < R; ++r) v[r] = table[c[r]];
+#pragma unroll
+  for (int r = 0; r < R; ++r) v[r] = valid ? v[r] : make_float4(nan, nan, nan, nan);
+  rms_finish_registers<R>(a.stats, a.apply, row, e.dst + long(row) * e.C, v, g);
+}
+// Number of float4 values per thread when the row fits in registers, else 0.
+__device__ __forceinline__ int row_registers(int C) {
+  return (C & 3) == 0 && C / 4 <= kRowRegisters * kBlock ? (C / 4 + kBlock - 1) / kBlock : 0;
+}
+
 __device__ void rms_stats__rms_apply_body(const RmsChainArgs &a, int block) {
   const int row = block;
   if (row >= a.stats.B) return;
@@ -310,6 +436,15 @@ __device__ void add__rms_stats__rms_apply_body(const AddRmsChainArgs &a, int blo
   const int row = block;
   if (row >= a.stats.B) return;
   const int C = a.stats.C;
+  if (a.x.parts <= kSourceBatch && a.y.parts <= kSourceBatch) {
+    switch (row_registers(C)) {
+      case 1: add_rms_registers<1>(a, row); return;
+      case 2: add_rms_registers<2>(a, row); return;
+      case 3: add_rms_registers<3>(a, row); return;
+      case 4: add_rms_registers<4>(a, row); return;
+      default: break;
+    }
+  }
   const long base = long(row) * C;
   float total = 0.f;
   if ((C & 3) == 0) {
@@ -338,6 +473,13 @@ __device__ void embedding__rms_stats__rms_apply_body(const EmbeddingRmsChainArgs
   if (row >= a.stats.B) return;
   const EmbeddingArgs &e = a.embedding;
   const int C = e.C;
+  switch (row_registers(C)) {
+    case 1: embedding_rms_registers<1>(a, row); return;
+    case 2: embedding_rms_registers<2>(a, row); return;
+    case 3: embedding_rms_registers<3>(a, row); return;
+    case 4: embedding_rms_registers<4>(a, row); return;
+    default: break;
+  }
   const int token = e.tokens[row];
   const bool valid = token >= 0 && token < e.V;
   const float nan = __builtin_nanf("");
@@ -1428,10 +1570,34 @@ CKL_ENTRY(silu, UnaryArgs, silu_body)
 
 // silu -> multiply as one launch of silu's geometry: element i (or float4 i) is activated,
 // written to silu's dst and multiplied by multiply's y in the same thread.
+// Both operands' loads (each at most kSourceBatch planes) issued before the activation.
+template <bool PlanesS, bool PlanesY> __device__ void silu_multiply_float4(const SiluMultiplyChainArgs &a, long i) {
+  const long idx[1] = {4 * i};
+  RowSource<1, PlanesS> src;
+  RowSource<1, PlanesY> y;
+  row_source_issue<1, PlanesS>(a.src, a.silu.src, idx, src);
+  row_source_issue<1, PlanesY>(a.y, a.multiply.y, idx, y);
+  const float4 v = row_source_value<1, PlanesS>(a.src, src, 0);
+  const float4 act = make_float4(silu(v.x), silu(v.y), silu(v.z), silu(v.w));
+  if (a.silu.dst) reinterpret_cast<float4 *>(a.silu.dst)[i] = act;   // null: only multiply reads it
+  const float4 u = row_source_value<1, PlanesY>(a.y, y, 0);
+  reinterpret_cast<float4 *>(a.multiply.dst)[i] =
+      make_float4(binary<1>(act.x, u.x), binary<1>(act.y, u.y), binary<1>(act.z, u.z), binary<1>(act.w, u.w));
+}
+
 __device__ void silu__multiply_body(const SiluMultiplyChainArgs &a, int block) {
   long i = long(block) * kBlock + threadIdx.x;
   const int n = a.silu.n;
-  if ((n & 3) == 0) {
+  if ((n & 3) == 0 && a.src.parts <= kSourceBatch && a.y.parts <= kSourceBatch) {
+    if (i >= n / 4) return;
+    if (a.src.parts > 0) {
+      if (a.y.parts > 0) silu_multiply_float4<true, true>(a, i);
+      else silu_multiply_float4<true, false>(a, i);
+    } else {
+      if (a.y.parts > 0) silu_multiply_float4<false, true>(a, i);
+      else silu_multiply_float4<false, false>(a, i);
+    }
+  } else if ((n & 3) == 0) {
     if (i >= n / 4) return;
     float4 v = source4(a.src, a.silu.src, 4 * i);
     float4 act = make_float4(silu(v.x), silu(v.y), silu(v.z), silu(v.w));
