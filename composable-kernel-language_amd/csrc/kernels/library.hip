@@ -1705,14 +1705,20 @@ CKL_ENTRY_ATTR(linear_rowvec__linear_rowvec__silu__multiply_nt, LinearSiluChainA
 // ------------------------------------------------------------------ greedy
 // tokens[b] = history[p, b] = first index of the maximum logit (strict '>' scan from index 0,
 // workloads.py:170-183): NaN logits never win, a NaN logit 0 is never displaced, +0 and -0 tie.
-// Each row is cut into `chunks` slices of kGreedyChunk logits, one 256-thread workgroup each.
-// A workgroup reduces its slice to a (value, index) pair; with one slice it writes the token,
-// otherwise it folds the pair into the row's 64-bit key (ordered value bits << 32 | ~index, so
-// the maximum key is the largest value at the smallest index) with an agent-scope atomic max
-// and bumps the row's counter; the last workgroup writes the token and resets key and counter.
+// A row of at most kGreedyRowLoads float4 per thread (V % 4 == 0; the library launches 1024
+// threads for rows above kGreedyChunk logits) is one workgroup: each thread scans its float4s
+// in index order with a strict '>' from -inf, so it keeps the first index of its maximum and
+// never takes a NaN, and the threads' (value, index) pairs are reduced as 64-bit keys (ordered
+// value bits << 32 | ~index: the maximum key is the largest value at the smallest index, -0 and
+// +0 tie). A row with no key above -inf (all -inf or NaN) and a row whose logit 0 is NaN pick 0.
+// Longer rows are cut into `chunks` slices of kGreedyChunk logits, one 256-thread workgroup
+// each, which fold their slice's key into the row's key with an agent-scope atomic max and bump
+// the row's counter; the last workgroup writes the token and resets key and counter.
 // workspace: uint64 key[B], uint32 counter[B], then the uint32 row count of the greedy ->
 // advance chain.
 constexpr int kGreedyChunk = 4096;
+constexpr int kGreedyRowLoads = 8;
+constexpr int kGreedyMaxWaves = 16;
 
 __device__ __forceinline__ unsigned long long greedy_key(float v, int index) {
   unsigned bits = __float_as_uint(v == 0.f ? 0.f : v);     // -0 ties with +0
@@ -1720,33 +1726,69 @@ __device__ __forceinline__ unsigned long long greedy_key(float v, int index) {
   return (static_cast<unsigned long long>(ordered) << 32) | (0xFFFFFFFFu - unsigned(index));
 }
 
+// The key of this thread's float4s of a one-workgroup row (see above).
+__device__ __forceinline__ unsigned long long greedy_row_key(const float *logits, int V) {
+  const float4 *row = reinterpret_cast<const float4 *>(logits);
+  const int n4 = V / 4, step = blockDim.x;
+  float4 x[kGreedyRowLoads];
+#pragma unroll
+  for (int u = 0; u < kGreedyRowLoads; ++u) x[u] = row[min(u * step + int(threadIdx.x), n4 - 1)];
+  float best = -__builtin_inff();
+  int index = -1;
+#pragma unroll
+  for (int u = 0; u < kGreedyRowLoads; ++u) {
+    const int c = u * step + int(threadIdx.x);
+    if (c < n4) {
+      const float v[4] = {x[u].x, x[u].y, x[u].z, x[u].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (v[e] > best) {
+          best = v[e];
+          index = 4 * c + e;
+        }
+    }
+  }
+  return index < 0 ? 0ull : greedy_key(best, index);
+}
+
 // Returns true in thread 0 of the workgroup that wrote row b's token; *position is the position
 // it read.
 __device__ __forceinline__ bool greedy_block(const GreedyArgs &a, int block, int *position) {
-  __shared__ unsigned long long bestKey[kBlock / 64];
+  __shared__ unsigned long long bestKey[kGreedyMaxWaves];
   const int b = block / a.chunks, chunk = block % a.chunks;
   if (b >= a.B) return false;
   const float *logits = a.logits + long(b) * a.V;
-  const int v0 = chunk * kGreedyChunk, v1 = min(v0 + kGreedyChunk, a.V);
+  // Thread 0 requests logit 0 and the position with the row, not after the reduction.
+  float first = 0.f;
+  int p = 0;
+  if (threadIdx.x == 0) {
+    first = logits[0];
+    p = load_position(a.position);
+  }
   unsigned long long key = 0;                               // below every real key
-  float x[kGreedyChunk / kBlock];
+  if (a.chunks == 1 && (a.V & 3) == 0 && a.V / 4 <= kGreedyRowLoads * int(blockDim.x)) {
+    key = greedy_row_key(logits, a.V);
+  } else {
+    const int v0 = chunk * kGreedyChunk, v1 = min(v0 + kGreedyChunk, a.V);
+    float x[kGreedyChunk / kBlock];
 #pragma unroll
-  for (int u = 0; u < kGreedyChunk / kBlock; ++u) x[u] = logits[min(v0 + u * kBlock + int(threadIdx.x), v1 - 1)];
+    for (int u = 0; u < kGreedyChunk / kBlock; ++u) x[u] = logits[min(v0 + u * kBlock + int(threadIdx.x), v1 - 1)];
 #pragma unroll
-  for (int u = 0; u < kGreedyChunk / kBlock; ++u) {
-    int k = v0 + u * kBlock + threadIdx.x;
-    if (k < v1 && x[u] == x[u]) key = max(key, greedy_key(x[u], k));
+    for (int u = 0; u < kGreedyChunk / kBlock; ++u) {
+      int k = v0 + u * kBlock + threadIdx.x;
+      if (k < v1 && x[u] == x[u]) key = max(key, greedy_key(x[u], k));
+    }
   }
 #pragma unroll
   for (int offset = 32; offset > 0; offset /= 2) {
     unsigned long long other = __shfl_xor(key, offset);
     key = max(key, other);
   }
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
   if (lane == 0) bestKey[wave] = key;
   __syncthreads();
   if (threadIdx.x != 0) return false;
-  for (int w = 1; w < kBlock / 64; ++w) key = max(key, bestKey[w]);
+  for (int w = 1; w < waves; ++w) key = max(key, bestKey[w]);
   bool finish = a.chunks == 1;
   if (!finish) {
     unsigned long long *keys = reinterpret_cast<unsigned long long *>(a.workspace);
@@ -1762,9 +1804,7 @@ __device__ __forceinline__ bool greedy_block(const GreedyArgs &a, int block, int
     }
   }
   if (!finish) return false;
-  float first = logits[0];
   int winner = (first != first || key == 0) ? 0 : int(0xFFFFFFFFu - unsigned(key & 0xFFFFFFFFu));
-  int p = load_position(a.position);
   a.tokens[b] = winner;
   if (p >= 0 && p < a.T) a.history[long(p) * a.B + b] = winner;
   *position = p;
@@ -1774,16 +1814,15 @@ __device__ void greedy_body(const GreedyArgs &a, int block) {
   int p;
   greedy_block(a, block, &p);
 }
-CKL_ENTRY(greedy, GreedyArgs, greedy_body)
+CKL_ENTRY_ATTR(greedy, GreedyArgs, greedy_body, 1024, )
 
 // greedy -> advance as one launch of greedy's geometry: the thread that writes a row's token
-// waits for its position load and stores to complete, then counts the row; the one that counts
-// the last row (every row has read the position by then) resets the count and stores
-// position + 1, which is what advance computes.
+// (its position load has returned: the history store's address uses it) counts the row; the one
+// that counts the last row (every row has read the position by then) resets the count and
+// stores position + 1, which is what advance computes.
 __device__ void greedy__advance_body(const GreedyAdvanceChainArgs &a, int block) {
   int p;
   if (!greedy_block(a.greedy, block, &p)) return;
-  __builtin_amdgcn_s_waitcnt(kWaitStores);
   unsigned *rows = reinterpret_cast<unsigned *>(a.greedy.workspace + 12 * a.greedy.B);
   unsigned previous = __hip_atomic_fetch_add(rows, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   if (previous == unsigned(a.greedy.B - 1)) {
@@ -1791,7 +1830,7 @@ __device__ void greedy__advance_body(const GreedyAdvanceChainArgs &a, int block)
     a.advance.position[0] = p + 1;
   }
 }
-CKL_ENTRY(greedy__advance, GreedyAdvanceChainArgs, greedy__advance_body)
+CKL_ENTRY_ATTR(greedy__advance, GreedyAdvanceChainArgs, greedy__advance_body, 1024, )
 
 // ------------------------------------------------------------------ advance
 // position[0] += 1   (workloads.py:186-188)

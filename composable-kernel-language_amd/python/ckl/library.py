@@ -217,6 +217,7 @@ def update(src: _Vector, dst: _Vector, bias: ckl.f32) -> None:
 BLOCK = 256
 VALUES_BLOCK = 512      # kValuesBlock: attention_values workgroup (one per (b, h))
 GREEDY_CHUNK = 4096     # kGreedyChunk: logits per greedy workgroup
+GREEDY_ROW_THREADS = 1024   # one workgroup per row of at most 8 float4 per thread (kGreedyRowLoads)
 
 
 def _cdiv(a: int, b: int) -> int:
@@ -397,8 +398,10 @@ def _greedy(shapes, consts, ext):
     (b, v), (t, _b) = shapes[0], shapes[2]
     if not (ext[0] >= b and ext[1:] == (1, 1)):
         return None
-    chunks = _cdiv(v, GREEDY_CHUNK)
     workspace = _cdiv(12 * b + 4, 256) * 256       # keys, counters, row count (greedy -> advance chain)
+    if GREEDY_CHUNK < v <= 8 * 4 * GREEDY_ROW_THREADS and v % 4 == 0:
+        return Launch(b, (b, v, t, 1), block=GREEDY_ROW_THREADS, workspace=workspace)
+    chunks = _cdiv(v, GREEDY_CHUNK)
     return Launch(b * chunks, (b, v, t, chunks), workspace=workspace)
 
 

@@ -63,6 +63,17 @@ def step(a, c):
     a["position"][0] += 1
 
 
+def greedy_scan(logits):
+    """Tokens of the CKL decoder's greedy kernel (benchmarks/decoder/workloads.py:170-183): per row,
+    a scan from index 0 keeps the running maximum and takes index v only when logit v is strictly
+    greater (`>`). So NaN never wins and a NaN logit 0 is never displaced, -0 and +0 tie, and equal
+    maxima keep the first index. On rows without NaN this is argmax (reference.py:71)."""
+    x = np.asarray(logits, np.float32)
+    y = np.where(np.isnan(x), -np.inf, x)
+    winner = np.argmax(y == y.max(axis=-1, keepdims=True), axis=-1)
+    return np.where(np.isnan(x[..., 0]), 0, winner).astype(np.int32)
+
+
 def initial_state(c, seed=123, *, init="reference", prompt_seed=None):
     """Weights, RoPE table, prompts and empty state before any prefill step."""
     rng = np.random.default_rng(seed)

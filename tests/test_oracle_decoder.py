@@ -47,3 +47,39 @@ def test_rms_and_softmax_closed_forms():
     oracle.step(arrays, c)
     assert int(arrays["position"][0]) == 1
     assert arrays["tokens"][0] == int(np.argmax(arrays["logits"][0]))
+
+
+def edge_rows(v, rng):
+    """Logit rows that exercise the greedy scan's rules: ties, NaN, -0/+0, -inf rows."""
+    rows = [rng.standard_normal(v).astype(np.float32) for _ in range(3)]
+    tie = np.full(v, -1.0, np.float32)
+    tie[[v // 3, v - 1]] = 2.0                                # equal maxima: the first index wins
+    nan0 = rng.standard_normal(v).astype(np.float32)
+    nan0[0] = np.nan                                          # NaN logit 0 is never displaced
+    nans = rng.standard_normal(v).astype(np.float32)
+    nans[rng.choice(v, v // 4, replace=False)] = np.nan
+    nans[v // 2] = 50.0                                       # NaN elsewhere never wins
+    zeros = np.full(v, -3.0, np.float32)
+    zeros[[2, v - 2]] = [-0.0, 0.0]                           # -0 and +0 tie
+    neg_inf = np.full(v, -np.inf, np.float32)                 # nothing beats logit 0
+    nan_inf = np.full(v, -np.inf, np.float32)
+    nan_inf[1::2] = np.nan
+    return np.stack(rows + [tie, nan0, nans, zeros, neg_inf, nan_inf])
+
+
+def scan_loop(row):
+    # The kernel body's loop, element by element (workloads.py:170-183).
+    best, winner = row[0], 0
+    for v in range(1, len(row)):
+        if row[v] > best:
+            best, winner = row[v], v
+    return winner
+
+
+@pytest.mark.parametrize("v", [5, 129, 4100])
+def test_greedy_scan_matches_the_scan_loop(v):
+    logits = edge_rows(v, np.random.default_rng(v))
+    expected = np.array([scan_loop(row) for row in logits], np.int32)
+    assert np.array_equal(oracle.greedy_scan(logits), expected)
+    clean = ~np.isnan(logits).any(axis=1)
+    assert np.array_equal(oracle.greedy_scan(logits[clean]), logits[clean].argmax(axis=1))
