@@ -1389,17 +1389,17 @@ __device__ __forceinline__ void score_key_batch(const KeyBatch &kb, const float4
 }
 
 // The scores -> softmax -> values row of (b, h) = bh with the query row `q` (global memory, or
-// LDS in the rope chain): scores into rowScores (LDS, T floats), softmax in place, values. With
+// LDS in the rope chain) at position `p` (sc.position[0], loaded by the caller): scores into
+// rowScores (LDS, T floats), softmax in place, values. With
 // `haveFirst`, `first` holds the wave's first batch of cache rows (vector layout only). With
 // `appended` (the rope chain, position in range), the key row at the position is read from LDS
 // instead of the cache and `storesPending` waves wait for their cache-row stores before the
 // barrier that precedes the values. The first batch of value rows is loaded before the softmax.
 template <bool NT, int P>
 __device__ __forceinline__ void attention_chain_row(const ScoresArgs &sc, const SoftmaxArgs &softmax,
-                                                    const ValuesArgs &values, long bh, const float *q,
+                                                    const ValuesArgs &values, long bh, const float *q, int p,
                                                     float *rowScores, const KeyBatch &first, bool haveFirst,
                                                     const float *appended = nullptr, bool storesPending = false) {
-  int p = load_position(sc.position);
   int end = min(p + 1, sc.T);
   if (p < 0) end = 0;
   const float *keys = sc.kc + (long(sc.layer) * sc.B * sc.A + bh) * long(sc.T) * sc.D;
@@ -1457,10 +1457,11 @@ __device__ void attention_scores__softmax__attention_values_body(const Attention
   if (bh >= long(a.values.B) * a.values.A) return;
   KeyBatch none;
   const float *q = a.scores.q + bh * a.scores.D;
+  const int p = load_position(a.scores.position);
   switch (score_pieces(a.scores.D)) {
-    case 1: attention_chain_row<NT, 1>(a.scores, a.softmax, a.values, bh, q, rowScores, none, false); break;
-    case 2: attention_chain_row<NT, 2>(a.scores, a.softmax, a.values, bh, q, rowScores, none, false); break;
-    default: attention_chain_row<NT, 4>(a.scores, a.softmax, a.values, bh, q, rowScores, none, false); break;
+    case 1: attention_chain_row<NT, 1>(a.scores, a.softmax, a.values, bh, q, p, rowScores, none, false); break;
+    case 2: attention_chain_row<NT, 2>(a.scores, a.softmax, a.values, bh, q, p, rowScores, none, false); break;
+    default: attention_chain_row<NT, 4>(a.scores, a.softmax, a.values, bh, q, p, rowScores, none, false); break;
   }
 }
 CKL_ENTRY_ATTR(attention_scores__softmax__attention_values, AttentionChainArgs,
@@ -1490,13 +1491,14 @@ __device__ void rope_attention_rows(const RopeAttentionChainArgs &a, int block) 
   float *krow = qrow + ap.D;
   const int p = load_position(q.position);
   const bool inRange = p >= 0 && p < q.T;
-  // The first batch of every wave's cache rows lies below p when p >= the batch stride: those
-  // loads are issued before the rotation and overlap it (the rows are not written here).
+  // Every wave's first batch of cache rows below p (rows >= p re-read an early row and are
+  // dropped, as in the scores loop) is requested before the rotation and overlaps it; this
+  // launch writes only row p of the cache.
   const int wave = threadIdx.x >> 6;
   const bool vector = scores_vector_layout(sc.D);
   const KeyLayout<P> layout(vector ? sc.D : 4 * P);
   const int firstBase = wave * layout.rowsPerBatch();
-  const bool early = vector && inRange && p >= int(blockDim.x >> 6) * layout.rowsPerBatch();
+  const bool early = vector && inRange && p >= 1;
   KeyBatch first;
   if (early)
     load_key_batch<NT, P>(first, sc.kc + (long(sc.layer) * sc.B * sc.A + bh) * long(sc.T) * sc.D, sc.D, layout,
@@ -1519,8 +1521,8 @@ __device__ void rope_attention_rows(const RopeAttentionChainArgs &a, int block) 
   __syncthreads();
   // The barrier alone does not wait for vector stores: the waves that appended cache rows wait for
   // them before the barrier that precedes the values (the scores take the key row from LDS).
-  attention_chain_row<NT, P>(a.scores, a.softmax, a.values, bh, inRange ? qrow : sc.q + bh * sc.D, rowScores, first,
-                             early, inRange ? krow : nullptr, inRange && int(threadIdx.x & ~63) < q.R);
+  attention_chain_row<NT, P>(a.scores, a.softmax, a.values, bh, inRange ? qrow : sc.q + bh * sc.D, p, rowScores,
+                             first, early, inRange ? krow : nullptr, inRange && int(threadIdx.x & ~63) < q.R);
 }
 template <bool NT> __device__ void rope_attention_stream(const RopeAttentionChainArgs &a, int block) {
   switch (score_pieces(a.scores.D)) {
@@ -1632,15 +1634,22 @@ template <bool NT> __device__ void linear_add_rms_stream(const LinearAddRmsChain
   const int waves = blockDim.x >> 6;
   const int C = a.stats.C;
   float *rowf = reinterpret_cast<float *>(row4);
+  const long base = long(b) * C;
+  const bool vec = (C & 3) == 0;
+  // The add's other operand and the gain are requested ahead of the linear's weights (every wave
+  // loads them, unpredicated at clamped indices; wave 0 uses them), so the row ops after the
+  // reduction wait for no further memory round trip.
+  const float *gain = a.apply.gain + long(a.apply.layer) * C;
+  const float other = (a.linearIsY ? a.add.x : a.add.y)[base + min(lane, C - 1)];
+  const float4 gain4 = vec ? reinterpret_cast<const float4 *>(gain)[min(lane, C / 4 - 1)] : make_float4(0.f, 0.f, 0.f, 0.f);
+  const float gain1 = gain[min(lane, C - 1)];
   red[wave][lane] = rowvec_partial<NT>(l, b, 0, 0);
   __syncthreads();
   if (wave != 0) return;
-  const long base = long(b) * C;
   if (lane < C) {
     float v = red[0][lane];
     for (int v2 = 1; v2 < waves; ++v2) v += red[v2][lane];
     if (l.dst) l.dst[long(b) * l.O + lane] = v;      // null: only add reads it
-    const float other = (a.linearIsY ? a.add.x : a.add.y)[base + lane];
     const float h = a.linearIsY ? binary<0>(other, v) : binary<0>(v, other);
     a.add.dst[base + lane] = h;
     rowf[lane] = h;
@@ -1648,7 +1657,6 @@ template <bool NT> __device__ void linear_add_rms_stream(const LinearAddRmsChain
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  const bool vec = (C & 3) == 0;
   float4 h4 = make_float4(0.f, 0.f, 0.f, 0.f);
   float h1 = 0.f, total = 0.f;
   if (vec) {
@@ -1664,13 +1672,10 @@ template <bool NT> __device__ void linear_add_rms_stream(const LinearAddRmsChain
   total = (total + 0.f) + (0.f + 0.f);               // block_sum over four waves, three of them empty
   const float s = rms_inverse(total, C, a.stats.eps);
   if (lane == 0 && a.stats.inv) a.stats.inv[b] = s;  // null: only the chain reads inv
-  const float *gain = a.apply.gain + long(a.apply.layer) * C;
   if (vec) {
-    if (lane < C / 4)
-      reinterpret_cast<float4 *>(a.apply.dst + base)[lane] =
-          rms_scale(h4, s, reinterpret_cast<const float4 *>(gain)[lane]);
+    if (lane < C / 4) reinterpret_cast<float4 *>(a.apply.dst + base)[lane] = rms_scale(h4, s, gain4);
   } else if (lane < C) {
-    a.apply.dst[base + lane] = h1 * s * gain[lane];
+    a.apply.dst[base + lane] = h1 * s * gain1;
   }
 }
 CKL_ENTRY_ATTR(linear_rowvec__add__rms_stats__rms_apply, LinearAddRmsChainArgs, linear_add_rms_stream<false>, 1024, )
