@@ -215,7 +215,10 @@ def kernel_roofline(session, c, samples=7):
                # rotated k, the attention's read of the rotated q, scores, probs
                "rope__rope__append_kv__attention_scores__softmax__attention_values": 12 * b * h + 16 * b * a * rows,
                "linear_rowvec__add__rms_stats__rms_apply": 8 * b * h,                 # linear output
-               "linear_rowvec__linear_rowvec__silu__multiply": 24 * b * f}            # gate, up, activation
+               "linear_rowvec__linear_rowvec__silu__multiply": 24 * b * f,            # gate, up, activation
+               # linear output, normalized row; gate, up, activation
+               "linear_rowvec__add__rms_stats__rms_apply__linear_rowvec__linear_rowvec__silu__multiply":
+                   16 * b * h + 24 * b * f}
     per_kernel = {}
     for index, (name, members) in enumerate(units):
         families = {nodes[m][0] for m in members}

@@ -100,6 +100,9 @@ struct CKL_ALIGN LinearAddRmsChainArgs {
 };
 // Two row-parallel linears of one x (gate, up; one slice) -> silu(gate) -> multiply by up.
 struct CKL_ALIGN LinearSiluChainArgs { LinearArgs gate; LinearArgs up; UnaryArgs silu; BinaryArgs multiply; };
+// The two row chains above in one launch for single-wave row-parallel linears (C <= 64): every
+// gate/up workgroup recomputes its row's linear -> add -> rms, the tile-0 workgroup writes them.
+struct CKL_ALIGN LinearAddRmsSiluChainArgs { LinearAddRmsChainArgs front; LinearSiluChainArgs back; };
 // rope(q), rope(k) -> append_kv -> attention_scores -> softmax -> attention_values per (b, h).
 struct CKL_ALIGN RopeAttentionChainArgs {
   RopeArgs q; RopeArgs k; AppendArgs append; ScoresArgs scores; SoftmaxArgs softmax; ValuesArgs values;

@@ -875,33 +875,47 @@ constexpr int kVectorRows = 64;
 constexpr int kVectorWaves = 16;
 // This wave's partial sum for output column tn*64 + lane of batch row b over its kVectorRows
 // reduction rows of slice kg (the caller combines the waves in wave order).
-template <bool NT> __device__ __forceinline__ float rowvec_partial(const LinearArgs &a, int b, int tn, int kg) {
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int waves = blockDim.x >> 6;
-  const int col = tn * 64 + lane;
-  const bool colOk = col < a.O;
+// A lane's reduction rows [k0, k1) and weight column of one chunk; the weights are loaded
+// (rows past k1 read the zero page) and then dotted with x, so x may come from memory or LDS.
+struct RowvecSlice { int k0, k1; const float *w; };
+__device__ __forceinline__ RowvecSlice rowvec_slice(const LinearArgs &a, int col, int chunk, int waves, int kg) {
   const int span = waves * kVectorRows;
   const int kb0 = kg * span, kb1 = min(kb0 + span, a.I);
-  const int k0 = kb0 + wave * kVectorRows, k1 = min(k0 + kVectorRows, kb1);
+  const int k0 = kb0 + chunk * kVectorRows, k1 = min(k0 + kVectorRows, kb1);
+  return {k0, k1, a.w + long(a.layer) * a.I * a.O + long(k0) * a.O + (col < a.O ? col : 0)};
+}
+template <bool NT>
+__device__ __forceinline__ void rowvec_load(const LinearArgs &a, const RowvecSlice &s, float (&wv)[kVectorRows]) {
   const float *zero = reinterpret_cast<const float *>(a.workspace);   // kZeroPage: 64 zero floats
-  const float *__restrict__ xr = a.x + long(b) * a.I;
-  const float *w = a.w + long(a.layer) * a.I * a.O + long(k0) * a.O + (colOk ? col : 0);
+  const int lane = threadIdx.x & 63;
+  if (s.k1 - s.k0 == kVectorRows) {
+#pragma unroll
+    for (int u = 0; u < kVectorRows; ++u) wv[u] = load1<NT>(s.w + long(u) * a.O);
+  } else if (s.k0 < s.k1) {
+#pragma unroll
+    for (int u = 0; u < kVectorRows; ++u) wv[u] = load1<NT>(s.k0 + u < s.k1 ? s.w + long(u) * a.O : zero + lane);
+  }
+}
+// x(k) is x[b, k] for k in [k0, k1).
+template <typename X>
+__device__ __forceinline__ float rowvec_dot(const RowvecSlice &s, const float (&wv)[kVectorRows], X x) {
   float acc = 0.f;
-  if (k1 - k0 == kVectorRows) {
-    float wv[kVectorRows];
+  if (s.k1 - s.k0 == kVectorRows) {
 #pragma unroll
-    for (int u = 0; u < kVectorRows; ++u) wv[u] = load1<NT>(w + long(u) * a.O);
+    for (int u = 0; u < kVectorRows; ++u) acc += x(s.k0 + u) * wv[u];
+  } else if (s.k0 < s.k1) {
 #pragma unroll
-    for (int u = 0; u < kVectorRows; ++u) acc += xr[k0 + u] * wv[u];
-  } else if (k0 < k1) {
-    float wv[kVectorRows];
-#pragma unroll
-    for (int u = 0; u < kVectorRows; ++u) wv[u] = load1<NT>(k0 + u < k1 ? w + long(u) * a.O : zero + lane);
-#pragma unroll
-    for (int u = 0; u < kVectorRows; ++u) acc += (k0 + u < k1 ? xr[min(k0 + u, k1 - 1)] : 0.f) * wv[u];
+    for (int u = 0; u < kVectorRows; ++u) acc += (s.k0 + u < s.k1 ? x(min(s.k0 + u, s.k1 - 1)) : 0.f) * wv[u];
   }
   return acc;
+}
+template <bool NT> __device__ __forceinline__ float rowvec_partial(const LinearArgs &a, int b, int tn, int kg) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const RowvecSlice s = rowvec_slice(a, tn * 64 + int(threadIdx.x & 63), wave, int(blockDim.x >> 6), kg);
+  const float *__restrict__ xr = a.x + long(b) * a.I;
+  float wv[kVectorRows];
+  rowvec_load<NT>(a, s, wv);
+  return rowvec_dot(s, wv, [&](int k) { return xr[k]; });
 }
 
 template <bool NT> __device__ void linear_rowvec_stream(const LinearArgs &a, int block) {
@@ -1706,6 +1720,91 @@ template <bool NT> __device__ void linear_silu_stream(const LinearSiluChainArgs 
 }
 CKL_ENTRY_ATTR(linear_rowvec__linear_rowvec__silu__multiply, LinearSiluChainArgs, linear_silu_stream<false>, 1024, )
 CKL_ENTRY_ATTR(linear_rowvec__linear_rowvec__silu__multiply_nt, LinearSiluChainArgs, linear_silu_stream<true>, 1024, )
+
+// linear -> add -> rms_stats -> rms_apply -> (linear, linear) -> silu -> multiply, for single-wave
+// row-parallel linears (64-thread blocks: C <= 64, so the first linear's rows and the normalized
+// row fit one wave): workgroup (tn, b) of the gate/up grid requests its gate and up weights with
+// the first linear's, recomputes row b's linear, add and rms exactly as the row chain does
+// (linear_add_rms_stream), keeps the normalized row in LDS as the x of its gate/up tile, and
+// finishes as linear_silu_stream. Only the tn = 0 workgroup writes the first chain's outputs (the
+// sum, inv, the normalized row and the linear's output, each unless the executor cleared it).
+template <bool NT> __device__ void linear_add_rms_silu_stream(const LinearAddRmsSiluChainArgs &a, int block) {
+  __shared__ float4 row4[16];
+  __shared__ float4 y4[16];
+  const LinearAddRmsChainArgs &f = a.front;
+  const LinearSiluChainArgs &k = a.back;
+  const LinearArgs &o = f.linear, &g = k.gate, &u = k.up;
+  const int tn = block % g.tilesN, b = block / g.tilesN;
+  if (b >= g.B) return;
+  const int lane = threadIdx.x & 63;
+  const int C = f.stats.C;
+  const bool writer = tn == 0;
+  float *rowf = reinterpret_cast<float *>(row4);
+  float *yf = reinterpret_cast<float *>(y4);
+  const long base = long(b) * C;
+  const bool vec = (C & 3) == 0;
+  const float *gain = f.apply.gain + long(f.apply.layer) * C;
+  const float other = (f.linearIsY ? f.add.x : f.add.y)[base + min(lane, C - 1)];
+  const float4 gain4 = vec ? reinterpret_cast<const float4 *>(gain)[min(lane, C / 4 - 1)] : make_float4(0.f, 0.f, 0.f, 0.f);
+  const float gain1 = gain[min(lane, C - 1)];
+  const RowvecSlice gs = rowvec_slice(g, tn * 64 + lane, 0, 1, 0), us = rowvec_slice(u, tn * 64 + lane, 0, 1, 0);
+  float gw[kVectorRows], uw[kVectorRows];
+  rowvec_load<NT>(g, gs, gw);
+  rowvec_load<NT>(u, us, uw);
+  const float v = rowvec_partial<NT>(o, b, 0, 0);
+  if (lane < C) {
+    if (writer && o.dst) o.dst[long(b) * o.O + lane] = v;   // null: only add reads it
+    const float h = f.linearIsY ? binary<0>(other, v) : binary<0>(v, other);
+    if (writer) f.add.dst[base + lane] = h;
+    rowf[lane] = h;
+  }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  float4 h4 = make_float4(0.f, 0.f, 0.f, 0.f);
+  float h1 = 0.f, total = 0.f;
+  if (vec) {
+    if (lane < C / 4) {
+      h4 = row4[lane];
+      total = add_squares(total, h4);
+    }
+  } else if (lane < C) {
+    h1 = rowf[lane];
+    total = __builtin_fmaf(h1, h1, total);
+  }
+  total = wave_sum(total);
+  total = (total + 0.f) + (0.f + 0.f);               // block_sum over four waves, three of them empty
+  const float s = rms_inverse(total, C, f.stats.eps);
+  if (writer && lane == 0 && f.stats.inv) f.stats.inv[b] = s;
+  if (vec) {
+    if (lane < C / 4) {
+      const float4 y = rms_scale(h4, s, gain4);
+      if (writer && f.apply.dst) reinterpret_cast<float4 *>(f.apply.dst + base)[lane] = y;
+      y4[lane] = y;
+    }
+  } else if (lane < C) {
+    const float y = h1 * s * gain1;
+    if (writer && f.apply.dst) f.apply.dst[base + lane] = y;
+    yf[lane] = y;
+  }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const float gv = rowvec_dot(gs, gw, [&](int kk) { return yf[kk]; });
+  const float uv = rowvec_dot(us, uw, [&](int kk) { return yf[kk]; });
+  const int col = tn * 64 + lane;
+  if (col >= g.O) return;
+  const long i = long(b) * g.O + col;
+  if (g.dst) g.dst[i] = gv;                          // null: only the chain reads them
+  if (u.dst) u.dst[i] = uv;
+  const float act = silu(gv);
+  if (k.silu.dst) k.silu.dst[i] = act;
+  k.multiply.dst[i] = binary<1>(act, uv);
+}
+CKL_ENTRY_ATTR(linear_rowvec__add__rms_stats__rms_apply__linear_rowvec__linear_rowvec__silu__multiply,
+               LinearAddRmsSiluChainArgs, linear_add_rms_silu_stream<false>, 64, )
+CKL_ENTRY_ATTR(linear_rowvec__add__rms_stats__rms_apply__linear_rowvec__linear_rowvec__silu__multiply_nt,
+               LinearAddRmsSiluChainArgs, linear_add_rms_silu_stream<true>, 64, )
 
 // ------------------------------------------------------------------ greedy
 // tokens[b] = history[p, b] = first index of the maximum logit (strict '>' scan from index 0,

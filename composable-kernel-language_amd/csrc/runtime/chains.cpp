@@ -7,7 +7,8 @@
 // rms_apply, silu -> multiply, rope(q), rope(k) -> append_kv -> attention_scores -> softmax ->
 // attention_values (or the rope part alone, attention_scores -> softmax -> attention_values, or
 // softmax -> attention_values), greedy -> advance, and for row-parallel linears whose workgroups
-// hold whole rows, linear -> add -> rms_stats -> rms_apply and linear, linear -> silu -> multiply. The plan itself (nodes, edges,
+// hold whole rows, linear -> add -> rms_stats -> rms_apply and linear, linear -> silu -> multiply
+// (both as one launch for single-wave linears). The plan itself (nodes, edges,
 // argument blocks) is unchanged; only the inferred lowering contracts a chain into one unit.
 //
 // A chain is taken only when
@@ -398,6 +399,51 @@ const char *linearSiluChain(const Members &m, const Internal &internal, Launch &
   return nullptr;
 }
 
+// The two row chains above as one launch when both linears are single-wave (64-thread blocks:
+// C <= 64): the gate/up grid, each workgroup recomputing its row's first chain. With several
+// workgroups per row, every range one of them writes must be disjoint from every other range.
+const char *linearAddRmsSiluChain(const Members &m, const Internal &internal, Launch &out) {
+  const Members front(m.begin(), m.begin() + 4), back(m.begin() + 4, m.end());
+  const Internal backInternal = [&](size_t index, const void *p) { return internal(index + 4, p); };
+  Launch f = out, k = out;
+  if (const char *why = linearAddRmsChain(front, internal, f)) return why;
+  if (const char *why = linearSiluChain(back, backInternal, k)) return why;
+  LinearAddRmsSiluChainArgs c{block<LinearAddRmsChainArgs>(f), block<LinearSiluChainArgs>(k)};
+  const LinearArgs &o = c.front.linear, &g = c.back.gate, &u = c.back.up;
+  if (f.block[0] != 64 || k.block[0] != 64) return "the linears are not single-wave row-parallel";
+  if (g.x != c.front.apply.dst || g.B != o.B || g.I != c.front.stats.C)
+    return "the gate and up linears do not multiply the normalized rows";
+  if (internal(3, c.front.apply.dst)) c.front.apply.dst = nullptr;
+  const uint64_t B = uint64_t(o.B), C = uint64_t(c.front.stats.C), F = uint64_t(g.O);
+  const BinaryArgs &ad = c.front.add;
+  std::vector<Range> ranges{whole(o.x, 4 * B * uint64_t(o.I)),
+                            whole(o.w + int64_t(o.layer) * o.I * o.O, 4ull * uint64_t(o.I) * uint64_t(o.O)),
+                            whole(c.front.linearIsY ? ad.x : ad.y, 4 * B * C),
+                            whole(c.front.apply.gain + int64_t(c.front.apply.layer) * int64_t(C), 4 * C),
+                            whole(g.w + int64_t(g.layer) * g.I * g.O, 4ull * uint64_t(g.I) * F),
+                            whole(u.w + int64_t(u.layer) * u.I * u.O, 4ull * uint64_t(u.I) * F),
+                            whole(o.workspace, kLinearZeroPage), whole(g.workspace, kLinearZeroPage),
+                            whole(u.workspace, kLinearZeroPage)};
+  std::vector<Range> written{whole(ad.dst, 4 * B * C), whole(c.back.multiply.dst, 4 * B * F)};
+  if (c.front.apply.dst) written.push_back(whole(c.front.apply.dst, 4 * B * C));
+  if (c.front.stats.inv) written.push_back(whole(c.front.stats.inv, 4 * B));
+  if (o.dst) written.push_back(whole(o.dst, 4 * B * C));
+  for (const void *p : {static_cast<const void *>(g.dst), static_cast<const void *>(u.dst),
+                        static_cast<const void *>(c.back.silu.dst)})
+    if (p) written.push_back(whole(p, 4 * B * F));
+  for (size_t i = 0; i < written.size(); ++i) {
+    for (size_t j = 0; j < ranges.size(); ++j)
+      if (!(written[i].end <= ranges[j].begin || ranges[j].end <= written[i].begin)) return kOverlap;
+    for (size_t j = i + 1; j < written.size(); ++j)
+      if (!(written[i].end <= written[j].begin || written[j].end <= written[i].begin)) return kOverlap;
+  }
+  out.grid[0] = k.grid[0];
+  out.block[0] = 64;
+  out.shared = 0;
+  setArguments(out, c);
+  return nullptr;
+}
+
 const char *greedyAdvanceChain(const Members &m, const Internal &, Launch &out) {
   GreedyAdvanceChainArgs c{block<GreedyArgs>(*m[0]), block<AdvanceArgs>(*m[1])};
   const GreedyArgs &g = c.greedy;
@@ -479,6 +525,34 @@ std::vector<size_t> matchRopeAttention(const Plan &plan, size_t head, const Succ
   return roles;
 }
 
+std::vector<size_t> matchLinearSilu(const Plan &plan, size_t head, const Successors &successors,
+                                    const std::vector<bool> &taken);
+
+// linear -> add -> rms_stats -> rms_apply (each the first direct successor of that name), then
+// the gate/up chain of a linear that reads the normalized rows.
+std::vector<size_t> matchLinearAddRmsSilu(const Plan &plan, size_t head, const Successors &successors,
+                                          const std::vector<bool> &taken) {
+  const size_t n = plan.nodes.size();
+  std::vector<size_t> roles{head};
+  for (const char *name : {"ckl_add", "ckl_rms_stats", "ckl_rms_apply"}) {
+    size_t found = n;
+    for (size_t s : successors[roles.back()]) {
+      const Launch &l = plan.nodes[s].launch;
+      if (!taken[s] && l.name == name && singleGrid(l) && s < found) found = s;
+    }
+    if (found == n) return {};
+    roles.push_back(found);
+  }
+  for (size_t s : successors[roles.back()]) {
+    std::vector<size_t> back = matchLinearSilu(plan, s, successors, taken);
+    if (back.size() == 4) {
+      roles.insert(roles.end(), back.begin(), back.end());
+      return roles;
+    }
+  }
+  return {};
+}
+
 // Two row-parallel linears of one x whose outputs meet in silu -> multiply: the head is the
 // linear silu reads (roles: gate, up, silu, multiply).
 std::vector<size_t> matchLinearSilu(const Plan &plan, size_t head, const Successors &successors,
@@ -527,6 +601,10 @@ const std::vector<Rule> &rules() {
        {{0, offsetof(RopeArgs, src), offsetof(RopeAttentionChainArgs, qsrc)},
         {1, offsetof(RopeArgs, src), offsetof(RopeAttentionChainArgs, ksrc)},
         {2, offsetof(AppendArgs, v), offsetof(RopeAttentionChainArgs, v)}}},
+      {{"ckl_linear_rowvec", "ckl_add", "ckl_rms_stats", "ckl_rms_apply", "ckl_linear_rowvec", "ckl_linear_rowvec",
+        "ckl_silu", "ckl_multiply"},
+       "ckl_linear_rowvec__add__rms_stats__rms_apply__linear_rowvec__linear_rowvec__silu__multiply",
+       linearAddRmsSiluChain, matchLinearAddRmsSilu},
       {{"ckl_linear_rowvec", "ckl_add", "ckl_rms_stats", "ckl_rms_apply"}, "ckl_linear_rowvec__add__rms_stats__rms_apply",
        linearAddRmsChain},
       {{"ckl_linear_rowvec", "ckl_linear_rowvec", "ckl_silu", "ckl_multiply"},
