@@ -1637,12 +1637,16 @@ CKL_ENTRY(silu__multiply, SiluMultiplyChainArgs, silu__multiply_body)
 // computed and combined exactly as linear_rowvec does. For the rms, C <= 64 keeps every value of
 // the row in wave 0, the only wave with data in the 256-thread rms kernels, and the sums follow
 // their order (float4 t or element t per thread, the wave sum, then the block sum's zeros).
-template <bool NT> __device__ void linear_add_rms_stream(const LinearAddRmsChainArgs &a, int block) {
+// Row b's linear -> add -> rms_stats -> rms_apply with the row-parallel linear's arithmetic (all
+// waves compute their chunk's partial; wave 0 adds them in wave order and finishes the row). Wave 0
+// leaves the normalized row in `y` (LDS, C floats) and returns true; the other waves return false
+// after the linear. Only a `writer` stores the chain's outputs (the linear's output, the sum, inv
+// and the normalized row, each unless the executor cleared its pointer).
+template <bool NT>
+__device__ __forceinline__ bool front_rows(const LinearAddRmsChainArgs &a, int b, bool writer, float4 *y) {
   __shared__ float red[kVectorWaves][64];
   __shared__ float4 row4[16];
   const LinearArgs &l = a.linear;
-  const int b = block;
-  if (b >= l.B) return;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int waves = blockDim.x >> 6;
@@ -1659,13 +1663,13 @@ template <bool NT> __device__ void linear_add_rms_stream(const LinearAddRmsChain
   const float gain1 = gain[min(lane, C - 1)];
   red[wave][lane] = rowvec_partial<NT>(l, b, 0, 0);
   __syncthreads();
-  if (wave != 0) return;
+  if (wave != 0) return false;
   if (lane < C) {
     float v = red[0][lane];
     for (int v2 = 1; v2 < waves; ++v2) v += red[v2][lane];
-    if (l.dst) l.dst[long(b) * l.O + lane] = v;      // null: only add reads it
+    if (writer && l.dst) l.dst[long(b) * l.O + lane] = v;   // null: only add reads it
     const float h = a.linearIsY ? binary<0>(other, v) : binary<0>(v, other);
-    a.add.dst[base + lane] = h;
+    if (writer) a.add.dst[base + lane] = h;
     rowf[lane] = h;
   }
   __builtin_amdgcn_wave_barrier();
@@ -1685,12 +1689,28 @@ template <bool NT> __device__ void linear_add_rms_stream(const LinearAddRmsChain
   total = wave_sum(total);
   total = (total + 0.f) + (0.f + 0.f);               // block_sum over four waves, three of them empty
   const float s = rms_inverse(total, C, a.stats.eps);
-  if (lane == 0 && a.stats.inv) a.stats.inv[b] = s;  // null: only the chain reads inv
+  if (writer && lane == 0 && a.stats.inv) a.stats.inv[b] = s;  // null: only the chain reads inv
   if (vec) {
-    if (lane < C / 4) reinterpret_cast<float4 *>(a.apply.dst + base)[lane] = rms_scale(h4, s, gain4);
+    if (lane < C / 4) {
+      const float4 r = rms_scale(h4, s, gain4);
+      if (writer && a.apply.dst) reinterpret_cast<float4 *>(a.apply.dst + base)[lane] = r;
+      y[lane] = r;
+    }
   } else if (lane < C) {
-    a.apply.dst[base + lane] = h1 * s * gain1;
+    const float r = h1 * s * gain1;
+    if (writer && a.apply.dst) a.apply.dst[base + lane] = r;
+    reinterpret_cast<float *>(y)[lane] = r;
   }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  return true;
+}
+
+template <bool NT> __device__ void linear_add_rms_stream(const LinearAddRmsChainArgs &a, int block) {
+  __shared__ float4 y[16];
+  if (block >= a.linear.B) return;
+  front_rows<NT>(a, block, true, y);
 }
 CKL_ENTRY_ATTR(linear_rowvec__add__rms_stats__rms_apply, LinearAddRmsChainArgs, linear_add_rms_stream<false>, 1024, )
 CKL_ENTRY_ATTR(linear_rowvec__add__rms_stats__rms_apply_nt, LinearAddRmsChainArgs, linear_add_rms_stream<true>, 1024, )
@@ -1724,72 +1744,22 @@ CKL_ENTRY_ATTR(linear_rowvec__linear_rowvec__silu__multiply_nt, LinearSiluChainA
 // linear -> add -> rms_stats -> rms_apply -> (linear, linear) -> silu -> multiply, for single-wave
 // row-parallel linears (64-thread blocks: C <= 64, so the first linear's rows and the normalized
 // row fit one wave): workgroup (tn, b) of the gate/up grid requests its gate and up weights with
-// the first linear's, recomputes row b's linear, add and rms exactly as the row chain does
-// (linear_add_rms_stream), keeps the normalized row in LDS as the x of its gate/up tile, and
-// finishes as linear_silu_stream. Only the tn = 0 workgroup writes the first chain's outputs (the
-// sum, inv, the normalized row and the linear's output, each unless the executor cleared it).
+// the first linear's, recomputes row b's first chain (front_rows), takes the normalized row from
+// LDS as the x of its gate/up tile, and finishes as linear_silu_stream. Only the tn = 0 workgroup
+// writes the first chain's outputs.
 template <bool NT> __device__ void linear_add_rms_silu_stream(const LinearAddRmsSiluChainArgs &a, int block) {
-  __shared__ float4 row4[16];
   __shared__ float4 y4[16];
-  const LinearAddRmsChainArgs &f = a.front;
   const LinearSiluChainArgs &k = a.back;
-  const LinearArgs &o = f.linear, &g = k.gate, &u = k.up;
+  const LinearArgs &g = k.gate, &u = k.up;
   const int tn = block % g.tilesN, b = block / g.tilesN;
   if (b >= g.B) return;
   const int lane = threadIdx.x & 63;
-  const int C = f.stats.C;
-  const bool writer = tn == 0;
-  float *rowf = reinterpret_cast<float *>(row4);
-  float *yf = reinterpret_cast<float *>(y4);
-  const long base = long(b) * C;
-  const bool vec = (C & 3) == 0;
-  const float *gain = f.apply.gain + long(f.apply.layer) * C;
-  const float other = (f.linearIsY ? f.add.x : f.add.y)[base + min(lane, C - 1)];
-  const float4 gain4 = vec ? reinterpret_cast<const float4 *>(gain)[min(lane, C / 4 - 1)] : make_float4(0.f, 0.f, 0.f, 0.f);
-  const float gain1 = gain[min(lane, C - 1)];
+  const float *yf = reinterpret_cast<const float *>(y4);
   const RowvecSlice gs = rowvec_slice(g, tn * 64 + lane, 0, 1, 0), us = rowvec_slice(u, tn * 64 + lane, 0, 1, 0);
   float gw[kVectorRows], uw[kVectorRows];
   rowvec_load<NT>(g, gs, gw);
   rowvec_load<NT>(u, us, uw);
-  const float v = rowvec_partial<NT>(o, b, 0, 0);
-  if (lane < C) {
-    if (writer && o.dst) o.dst[long(b) * o.O + lane] = v;   // null: only add reads it
-    const float h = f.linearIsY ? binary<0>(other, v) : binary<0>(v, other);
-    if (writer) f.add.dst[base + lane] = h;
-    rowf[lane] = h;
-  }
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  float4 h4 = make_float4(0.f, 0.f, 0.f, 0.f);
-  float h1 = 0.f, total = 0.f;
-  if (vec) {
-    if (lane < C / 4) {
-      h4 = row4[lane];
-      total = add_squares(total, h4);
-    }
-  } else if (lane < C) {
-    h1 = rowf[lane];
-    total = __builtin_fmaf(h1, h1, total);
-  }
-  total = wave_sum(total);
-  total = (total + 0.f) + (0.f + 0.f);               // block_sum over four waves, three of them empty
-  const float s = rms_inverse(total, C, f.stats.eps);
-  if (writer && lane == 0 && f.stats.inv) f.stats.inv[b] = s;
-  if (vec) {
-    if (lane < C / 4) {
-      const float4 y = rms_scale(h4, s, gain4);
-      if (writer && f.apply.dst) reinterpret_cast<float4 *>(f.apply.dst + base)[lane] = y;
-      y4[lane] = y;
-    }
-  } else if (lane < C) {
-    const float y = h1 * s * gain1;
-    if (writer && f.apply.dst) f.apply.dst[base + lane] = y;
-    yf[lane] = y;
-  }
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  if (!front_rows<NT>(a.front, b, tn == 0, y4)) return;
   const float gv = rowvec_dot(gs, gw, [&](int kk) { return yf[kk]; });
   const float uv = rowvec_dot(us, uw, [&](int kk) { return yf[kk]; });
   const int col = tn * 64 + lane;
