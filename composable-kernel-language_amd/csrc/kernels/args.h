@@ -103,6 +103,9 @@ struct CKL_ALIGN LinearSiluChainArgs { LinearArgs gate; LinearArgs up; UnaryArgs
 // The two row chains above in one launch for single-wave row-parallel linears (C <= 64): every
 // gate/up workgroup recomputes its row's linear -> add -> rms, the tile-0 workgroup writes them.
 struct CKL_ALIGN LinearAddRmsSiluChainArgs { LinearAddRmsChainArgs front; LinearSiluChainArgs back; };
+// embedding -> rms_stats -> rms_apply, then `count` (1 to 3) single-wave row-parallel linears of
+// the normalized rows (layer 0's q, k, v): member m owns blocks [start[m], start[m+1]).
+struct CKL_ALIGN EmbeddingRmsLinearsChainArgs { EmbeddingRmsChainArgs front; LinearArgs back[3]; int count, start[4], pad; };
 // rope(q), rope(k) -> append_kv -> attention_scores -> softmax -> attention_values per (b, h).
 struct CKL_ALIGN RopeAttentionChainArgs {
   RopeArgs q; RopeArgs k; AppendArgs append; ScoresArgs scores; SoftmaxArgs softmax; ValuesArgs values;

@@ -1776,6 +1776,59 @@ CKL_ENTRY_ATTR(linear_rowvec__add__rms_stats__rms_apply__linear_rowvec__linear_r
 CKL_ENTRY_ATTR(linear_rowvec__add__rms_stats__rms_apply__linear_rowvec__linear_rowvec__silu__multiply_nt,
                LinearAddRmsSiluChainArgs, linear_add_rms_silu_stream<true>, 64, )
 
+// embedding -> rms_stats -> rms_apply -> `count` single-wave row-parallel linears of the normalized
+// rows, C <= 64 and C % 4 == 0 (64-thread blocks): member m owns blocks [start[m], start[m+1]) of
+// its tilesN x B grid. Each workgroup requests its tile's weights, gathers its row's embedding (a
+// float4 per lane) and normalizes it with the chain's arithmetic (the 256-thread row's block sum,
+// in which only wave 0 holds data), then computes its tile from the normalized row in LDS with the
+// single-wave linear's arithmetic. Member 0's tile-0 workgroups write the row chain's outputs.
+template <bool NT> __device__ void embedding_rms_linears_stream(const EmbeddingRmsLinearsChainArgs &a, int block) {
+  __shared__ float4 y4[16];
+  int m = 0;
+  while (m + 1 < a.count && block >= a.start[m + 1]) ++m;
+  const LinearArgs &l = a.back[m];
+  const int local = block - a.start[m];
+  const int tn = local % l.tilesN, b = local / l.tilesN;
+  if (b >= l.B) return;
+  const int lane = threadIdx.x & 63;
+  const RowvecSlice ls = rowvec_slice(l, tn * 64 + lane, 0, 1, 0);
+  float lw[kVectorRows];
+  rowvec_load<NT>(l, ls, lw);
+  const EmbeddingRmsChainArgs &f = a.front;
+  const EmbeddingArgs &e = f.embedding;
+  const int n4 = e.C / 4, c = min(lane, n4 - 1);
+  const float4 g = reinterpret_cast<const float4 *>(f.apply.gain + long(f.apply.layer) * e.C)[c];
+  const int token = e.tokens[b];
+  const bool valid = token >= 0 && token < e.V;
+  const float nan = __builtin_nanf("");
+  float4 v = reinterpret_cast<const float4 *>(e.table + long(valid ? token : 0) * e.C)[c];
+  v = valid ? v : make_float4(nan, nan, nan, nan);
+  float total = lane < n4 ? add_squares(0.f, v) : 0.f;
+  total = wave_sum(total);
+  total = (total + 0.f) + (0.f + 0.f);               // block_sum over four waves, three of them empty
+  const float s = rms_inverse(total, e.C, f.stats.eps);
+  const float4 y = rms_scale(v, s, g);
+  if (m == 0 && tn == 0) {
+    if (lane < n4) {
+      reinterpret_cast<float4 *>(e.dst + long(b) * e.C)[lane] = v;
+      if (f.apply.dst) reinterpret_cast<float4 *>(f.apply.dst + long(b) * e.C)[lane] = y;
+    }
+    if (lane == 0 && f.stats.inv) f.stats.inv[b] = s;   // null: only the chain reads inv
+  }
+  if (lane < n4) y4[lane] = y;
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const float *yf = reinterpret_cast<const float *>(y4);
+  const float out = rowvec_dot(ls, lw, [&](int kk) { return yf[kk]; });
+  const int col = tn * 64 + lane;
+  if (col < l.O && l.dst) l.dst[long(b) * l.O + col] = out;
+}
+CKL_ENTRY_ATTR(embedding__rms_stats__rms_apply__linear_rowvec__linear_rowvec__linear_rowvec,
+               EmbeddingRmsLinearsChainArgs, embedding_rms_linears_stream<false>, 64, )
+CKL_ENTRY_ATTR(embedding__rms_stats__rms_apply__linear_rowvec__linear_rowvec__linear_rowvec_nt,
+               EmbeddingRmsLinearsChainArgs, embedding_rms_linears_stream<true>, 64, )
+
 // ------------------------------------------------------------------ greedy
 // tokens[b] = history[p, b] = first index of the maximum logit (strict '>' scan from index 0,
 // workloads.py:170-183): NaN logits never win, a NaN logit 0 is never displaced, +0 and -0 tie.

@@ -444,6 +444,55 @@ const char *linearAddRmsSiluChain(const Members &m, const Internal &internal, La
   return nullptr;
 }
 
+// embedding -> rms_stats -> rms_apply, then single-wave row-parallel linears of the normalized rows
+// (layer 0's q, k, v) as one launch of the linears' grids (C <= 64, C % 4 == 0), every workgroup
+// recomputing its row's gather and rms. Several workgroups per row: written ranges must be
+// disjoint from every other range.
+const char *embeddingRmsLinearsChain(const Members &m, const Internal &internal, Launch &out) {
+  const Members front(m.begin(), m.begin() + 3);
+  Launch f = out;
+  if (const char *why = embeddingRmsChain(front, internal, f)) return why;
+  EmbeddingRmsLinearsChainArgs c{};
+  c.front = block<EmbeddingRmsChainArgs>(f);
+  const EmbeddingArgs &e = c.front.embedding;
+  if (e.C % 4 || e.C > 64) return "the embedding row does not fit one wave's float4s";
+  c.count = int(m.size() - 3);
+  if (c.count < 1 || c.count > 3) return "the chain takes one to three linears";
+  const uint64_t B = uint64_t(e.B), C = uint64_t(e.C);
+  std::vector<Range> ranges{whole(e.tokens, 4 * B), whole(e.table, uint64_t(e.V) * 4 * C),
+                            whole(c.front.apply.gain + int64_t(c.front.apply.layer) * int64_t(C), 4 * C)};
+  std::vector<Range> written{whole(e.dst, 4 * B * C)};
+  int start = 0;
+  for (int k = 0; k < c.count; ++k) {
+    const Launch &ll = *m[3 + size_t(k)];
+    if (ll.arguments.size() != sizeof(LinearArgs)) return "a linear's block does not match the library layout";
+    LinearArgs &l = c.back[k] = block<LinearArgs>(ll);
+    if (ll.block[0] != 64 || l.kSplit != 1 || l.x != c.front.apply.dst || l.B != e.B || l.I != e.C || l.O <= 0 ||
+        !l.workspace || ll.grid[0] != unsigned(l.tilesN) * unsigned(l.B))
+      return "a linear is not a single-wave row-parallel projection of the normalized rows";
+    c.start[k] = start;
+    start += int(ll.grid[0]);
+    ranges.push_back(whole(l.w + int64_t(l.layer) * l.I * l.O, 4ull * uint64_t(l.I) * uint64_t(l.O)));
+    ranges.push_back(whole(l.workspace, kLinearZeroPage));
+    if (l.dst) written.push_back(whole(l.dst, 4 * B * uint64_t(l.O)));
+  }
+  for (int k = c.count; k <= 3; ++k) c.start[k] = start;
+  if (internal(2, c.front.apply.dst)) c.front.apply.dst = nullptr;
+  if (c.front.apply.dst) written.push_back(whole(c.front.apply.dst, 4 * B * C));
+  if (c.front.stats.inv) written.push_back(whole(c.front.stats.inv, 4 * B));
+  for (size_t i = 0; i < written.size(); ++i) {
+    for (size_t j = 0; j < ranges.size(); ++j)
+      if (!(written[i].end <= ranges[j].begin || ranges[j].end <= written[i].begin)) return kOverlap;
+    for (size_t j = i + 1; j < written.size(); ++j)
+      if (!(written[i].end <= written[j].begin || written[j].end <= written[i].begin)) return kOverlap;
+  }
+  out.grid[0] = unsigned(start);
+  out.block[0] = 64;
+  out.shared = 0;
+  setArguments(out, c);
+  return nullptr;
+}
+
 const char *greedyAdvanceChain(const Members &m, const Internal &, Launch &out) {
   GreedyAdvanceChainArgs c{block<GreedyArgs>(*m[0]), block<AdvanceArgs>(*m[1])};
   const GreedyArgs &g = c.greedy;
@@ -553,6 +602,37 @@ std::vector<size_t> matchLinearAddRmsSilu(const Plan &plan, size_t head, const S
   return {};
 }
 
+// embedding -> rms_stats -> rms_apply (each the first direct successor of that name), then the
+// three row-parallel linears that multiply the normalized rows (in plan order).
+std::vector<size_t> matchEmbeddingRmsLinears(const Plan &plan, size_t head, const Successors &successors,
+                                             const std::vector<bool> &taken) {
+  const size_t n = plan.nodes.size();
+  std::vector<size_t> roles{head};
+  for (const char *name : {"ckl_rms_stats", "ckl_rms_apply"}) {
+    size_t found = n;
+    for (size_t s : successors[roles.back()]) {
+      const Launch &l = plan.nodes[s].launch;
+      if (!taken[s] && l.name == name && singleGrid(l) && s < found) found = s;
+    }
+    if (found == n) return {};
+    roles.push_back(found);
+  }
+  const Launch &apply = plan.nodes[roles.back()].launch;
+  if (apply.arguments.size() != sizeof(RmsApplyArgs)) return {};
+  const void *y = block<RmsApplyArgs>(apply).dst;
+  std::vector<size_t> linears;
+  for (size_t s : successors[roles.back()]) {
+    const Launch &l = plan.nodes[s].launch;
+    if (!taken[s] && l.name == "ckl_linear_rowvec" && singleGrid(l) && l.arguments.size() == sizeof(LinearArgs) &&
+        block<LinearArgs>(l).x == y)
+      linears.push_back(s);
+  }
+  if (linears.size() != 3) return {};
+  std::sort(linears.begin(), linears.end());
+  roles.insert(roles.end(), linears.begin(), linears.end());
+  return roles;
+}
+
 // Two row-parallel linears of one x whose outputs meet in silu -> multiply: the head is the
 // linear silu reads (roles: gate, up, silu, multiply).
 std::vector<size_t> matchLinearSilu(const Plan &plan, size_t head, const Successors &successors,
@@ -611,6 +691,9 @@ const std::vector<Rule> &rules() {
        "ckl_linear_rowvec__linear_rowvec__silu__multiply", linearSiluChain, matchLinearSilu},
       {{"ckl_add", "ckl_rms_stats", "ckl_rms_apply"}, "ckl_add__rms_stats__rms_apply", addRmsChain, nullptr,
        {{0, offsetof(BinaryArgs, x), offsetof(AddRmsChainArgs, x)}, {0, offsetof(BinaryArgs, y), offsetof(AddRmsChainArgs, y)}}},
+      {{"ckl_embedding", "ckl_rms_stats", "ckl_rms_apply", "ckl_linear_rowvec", "ckl_linear_rowvec", "ckl_linear_rowvec"},
+       "ckl_embedding__rms_stats__rms_apply__linear_rowvec__linear_rowvec__linear_rowvec", embeddingRmsLinearsChain,
+       matchEmbeddingRmsLinears},
       {{"ckl_embedding", "ckl_rms_stats", "ckl_rms_apply"}, "ckl_embedding__rms_stats__rms_apply", embeddingRmsChain},
       {{"ckl_rms_stats", "ckl_rms_apply"}, "ckl_rms_stats__rms_apply", rmsChain},
       {{"ckl_silu", "ckl_multiply"}, "ckl_silu__multiply", siluMultiplyChain, nullptr,
