@@ -219,7 +219,8 @@ def kernel_roofline(session, c, samples=7):
                # linear output, normalized row; gate, up, activation
                "linear_rowvec__add__rms_stats__rms_apply__linear_rowvec__linear_rowvec__silu__multiply":
                    16 * b * h + 24 * b * f,
-               "embedding__rms_stats__rms_apply__linear_rowvec__linear_rowvec__linear_rowvec": 8 * b * h}   # normalized row
+               "embedding__rms_stats__rms_apply__linear_rowvec__linear_rowvec__linear_rowvec": 8 * b * h,  # normalized row
+               "linear_rowvec__greedy__advance": 4 * b * c.vocab}                  # greedy's read of the logits
     per_kernel = {}
     for index, (name, members) in enumerate(units):
         families = {nodes[m][0] for m in members}

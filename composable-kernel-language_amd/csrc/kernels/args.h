@@ -106,6 +106,9 @@ struct CKL_ALIGN LinearAddRmsSiluChainArgs { LinearAddRmsChainArgs front; Linear
 // embedding -> rms_stats -> rms_apply, then `count` (1 to 3) single-wave row-parallel linears of
 // the normalized rows (layer 0's q, k, v): member m owns blocks [start[m], start[m+1]).
 struct CKL_ALIGN EmbeddingRmsLinearsChainArgs { EmbeddingRmsChainArgs front; LinearArgs back[3]; int count, start[4], pad; };
+// A single-wave row-parallel linear whose output row feeds greedy -> advance (the LM head): one
+// workgroup per row, one wave per 64-column tile.
+struct CKL_ALIGN LinearGreedyAdvanceChainArgs { LinearArgs linear; GreedyAdvanceChainArgs pick; };
 // rope(q), rope(k) -> append_kv -> attention_scores -> softmax -> attention_values per (b, h).
 struct CKL_ALIGN RopeAttentionChainArgs {
   RopeArgs q; RopeArgs k; AppendArgs append; ScoresArgs scores; SoftmaxArgs softmax; ValuesArgs values;

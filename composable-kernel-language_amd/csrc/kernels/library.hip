@@ -1959,6 +1959,47 @@ __device__ void greedy__advance_body(const GreedyAdvanceChainArgs &a, int block)
 }
 CKL_ENTRY_ATTR(greedy__advance, GreedyAdvanceChainArgs, greedy__advance_body, 1024, )
 
+// linear -> greedy -> advance for a single-wave row-parallel linear of at most 16 tiles (the LM head
+// of a narrow decoder): workgroup b computes row b's logits, wave w the columns of tile w with the
+// linear's arithmetic, writes them, and picks the token from the values in registers: each lane's
+// key (value bits, ~column) when its logit is above -inf, reduced as greedy_block does (logit 0
+// NaN or no key above -inf: token 0); the row is then counted as in greedy__advance_body.
+template <bool NT> __device__ void linear_greedy_advance_stream(const LinearGreedyAdvanceChainArgs &a, int block) {
+  __shared__ unsigned long long bestKey[kGreedyMaxWaves];
+  const LinearArgs &l = a.linear;
+  const GreedyArgs &g = a.pick.greedy;
+  const int b = block;
+  if (b >= l.B) return;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), waves = blockDim.x >> 6;
+  int p = 0;
+  if (threadIdx.x == 0) p = load_position(g.position);
+  const int col = wave * 64 + lane;
+  const RowvecSlice sl = rowvec_slice(l, col, 0, 1, 0);
+  const float *__restrict__ xr = l.x + long(b) * l.I;
+  float wv[kVectorRows];
+  rowvec_load<NT>(l, sl, wv);
+  const float v = rowvec_dot(sl, wv, [&](int k) { return xr[k]; });
+  if (col < l.O) l.dst[long(b) * l.O + col] = v;
+  unsigned long long key = col < g.V && v > -__builtin_inff() ? greedy_key(v, col) : 0ull;
+#pragma unroll
+  for (int offset = 32; offset > 0; offset /= 2) key = max(key, __shfl_xor(key, offset));
+  if (lane == 0) bestKey[wave] = key;
+  __syncthreads();
+  if (threadIdx.x != 0) return;
+  for (int w = 1; w < waves; ++w) key = max(key, bestKey[w]);
+  const int winner = (v != v || key == 0) ? 0 : int(0xFFFFFFFFu - unsigned(key & 0xFFFFFFFFu));   // v: logit 0
+  g.tokens[b] = winner;
+  if (p >= 0 && p < g.T) g.history[long(p) * g.B + b] = winner;
+  unsigned *rows = reinterpret_cast<unsigned *>(g.workspace + 12 * g.B);
+  if (__hip_atomic_fetch_add(rows, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == unsigned(g.B - 1)) {
+    __hip_atomic_store(rows, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    a.pick.advance.position[0] = p + 1;
+  }
+}
+CKL_ENTRY_ATTR(linear_rowvec__greedy__advance, LinearGreedyAdvanceChainArgs, linear_greedy_advance_stream<false>, 1024, )
+CKL_ENTRY_ATTR(linear_rowvec__greedy__advance_nt, LinearGreedyAdvanceChainArgs, linear_greedy_advance_stream<true>, 1024, )
+
 // ------------------------------------------------------------------ advance
 // position[0] += 1   (workloads.py:186-188)
 __device__ void advance_body(const AdvanceArgs &a, int block) {

@@ -444,6 +444,38 @@ const char *linearAddRmsSiluChain(const Members &m, const Internal &internal, La
   return nullptr;
 }
 
+const char *greedyAdvanceChain(const Members &m, const Internal &, Launch &out);
+
+// A single-wave row-parallel linear of at most 16 tiles whose output rows are greedy's logits, then
+// greedy -> advance: one workgroup per row (one wave per tile); the logits are still written.
+const char *linearGreedyAdvanceChain(const Members &m, const Internal &internal, Launch &out) {
+  const Members tail(m.begin() + 1, m.end());
+  const Internal shifted = [&](size_t index, const void *p) { return internal(index + 1, p); };
+  Launch pick = out;
+  if (const char *why = greedyAdvanceChain(tail, shifted, pick)) return why;
+  if (m[0]->arguments.size() != sizeof(LinearArgs)) return "the linear's block does not match the library layout";
+  LinearGreedyAdvanceChainArgs c{block<LinearArgs>(*m[0]), block<GreedyAdvanceChainArgs>(pick)};
+  const LinearArgs &l = c.linear;
+  const GreedyArgs &g = c.pick.greedy;
+  if (m[0]->block[0] != 64 || l.kSplit != 1 || l.tilesN < 1 || l.tilesN > 16 || l.dst != g.logits || l.O != g.V ||
+      l.B != g.B || g.chunks != 1 || !l.workspace || m[0]->grid[0] != unsigned(l.tilesN) * unsigned(l.B))
+    return "the linear is not a single-wave row-parallel projection to greedy's logits";
+  const uint64_t B = uint64_t(l.B), V = uint64_t(l.O);
+  const std::vector<Range> read{whole(l.x, 4 * B * uint64_t(l.I)),
+                                whole(l.w + int64_t(l.layer) * l.I * l.O, 4ull * uint64_t(l.I) * V),
+                                whole(l.workspace, kLinearZeroPage)};
+  const std::vector<Range> written{whole(l.dst, 4 * B * V), whole(g.tokens, 4 * B),
+                                   whole(g.history, 4ull * uint64_t(g.T) * B), whole(g.position, 4)};
+  for (const Range &w : written)
+    for (const Range &r : read)
+      if (!(w.end <= r.begin || r.end <= w.begin)) return kOverlap;
+  out.grid[0] = unsigned(l.B);
+  out.block[0] = 64u * unsigned(l.tilesN);
+  out.shared = 0;
+  setArguments(out, c);
+  return nullptr;
+}
+
 // embedding -> rms_stats -> rms_apply, then single-wave row-parallel linears of the normalized rows
 // (layer 0's q, k, v) as one launch of the linears' grids (C <= 64, C % 4 == 0), every workgroup
 // recomputing its row's gather and rms. Several workgroups per row: written ranges must be
@@ -702,6 +734,8 @@ const std::vector<Rule> &rules() {
       {{"ckl_attention_scores", "ckl_softmax", "ckl_attention_values"}, "ckl_attention_scores__softmax__attention_values",
        attentionChain},
       {{"ckl_softmax", "ckl_attention_values"}, "ckl_softmax__attention_values", softmaxValuesChain},
+      {{"ckl_linear_rowvec", "ckl_greedy", "ckl_advance"}, "ckl_linear_rowvec__greedy__advance",
+       linearGreedyAdvanceChain},
       {{"ckl_greedy", "ckl_advance"}, "ckl_greedy__advance", greedyAdvanceChain},
       {{"ckl_rope", "ckl_rope", "ckl_append_kv"}, "ckl_rope__rope__append_kv", ropeAppendChain, matchRopeAppend,
        {{0, offsetof(RopeArgs, src), offsetof(RopeAppendChainArgs, qsrc)},
