@@ -79,6 +79,19 @@ bool hazardFree(const std::vector<Range> &ranges) {
   return true;
 }
 
+// For launches in which several workgroups touch one row: every written range is disjoint from
+// every other written range and from every range in `others` (no identical-rows exception).
+bool writesDisjoint(const std::vector<Range> &written, const std::vector<Range> &others) {
+  auto apart = [](const Range &a, const Range &b) { return a.end <= b.begin || b.end <= a.begin; };
+  for (size_t i = 0; i < written.size(); ++i) {
+    for (const Range &r : others)
+      if (!apart(written[i], r)) return false;
+    for (size_t j = i + 1; j < written.size(); ++j)
+      if (!apart(written[i], written[j])) return false;
+  }
+  return true;
+}
+
 template <typename T> T block(const Launch &launch) {
   // Packed blocks are padded to 8 bytes, as are the aligned(8) structs.
   if (launch.arguments.size() != sizeof(T))
@@ -431,12 +444,7 @@ const char *linearAddRmsSiluChain(const Members &m, const Internal &internal, La
   for (const void *p : {static_cast<const void *>(g.dst), static_cast<const void *>(u.dst),
                         static_cast<const void *>(c.back.silu.dst)})
     if (p) written.push_back(whole(p, 4 * B * F));
-  for (size_t i = 0; i < written.size(); ++i) {
-    for (size_t j = 0; j < ranges.size(); ++j)
-      if (!(written[i].end <= ranges[j].begin || ranges[j].end <= written[i].begin)) return kOverlap;
-    for (size_t j = i + 1; j < written.size(); ++j)
-      if (!(written[i].end <= written[j].begin || written[j].end <= written[i].begin)) return kOverlap;
-  }
+  if (!writesDisjoint(written, ranges)) return kOverlap;
   out.grid[0] = k.grid[0];
   out.block[0] = 64;
   out.shared = 0;
@@ -466,9 +474,7 @@ const char *linearGreedyAdvanceChain(const Members &m, const Internal &internal,
                                 whole(l.workspace, kLinearZeroPage)};
   const std::vector<Range> written{whole(l.dst, 4 * B * V), whole(g.tokens, 4 * B),
                                    whole(g.history, 4ull * uint64_t(g.T) * B), whole(g.position, 4)};
-  for (const Range &w : written)
-    for (const Range &r : read)
-      if (!(w.end <= r.begin || r.end <= w.begin)) return kOverlap;
+  if (!writesDisjoint(written, read)) return kOverlap;
   out.grid[0] = unsigned(l.B);
   out.block[0] = 64u * unsigned(l.tilesN);
   out.shared = 0;
@@ -512,12 +518,7 @@ const char *embeddingRmsLinearsChain(const Members &m, const Internal &internal,
   if (internal(2, c.front.apply.dst)) c.front.apply.dst = nullptr;
   if (c.front.apply.dst) written.push_back(whole(c.front.apply.dst, 4 * B * C));
   if (c.front.stats.inv) written.push_back(whole(c.front.stats.inv, 4 * B));
-  for (size_t i = 0; i < written.size(); ++i) {
-    for (size_t j = 0; j < ranges.size(); ++j)
-      if (!(written[i].end <= ranges[j].begin || ranges[j].end <= written[i].begin)) return kOverlap;
-    for (size_t j = i + 1; j < written.size(); ++j)
-      if (!(written[i].end <= written[j].begin || written[j].end <= written[i].begin)) return kOverlap;
-  }
+  if (!writesDisjoint(written, ranges)) return kOverlap;
   out.grid[0] = unsigned(start);
   out.block[0] = 64;
   out.shared = 0;
