@@ -5,25 +5,40 @@ For each decoder configuration (small, wide, deep, large) the dec
 lowered, compiled with storage reuse off and on, bound to device-resident synthetic state,
 prefilled on the GPU (teacher-forced prompt), and timed per variant with the protocol of the
 reference harness (benchmarks/decoder/run.py:160-197): every sample resets the mutable state and
-times one 16-step generation with HIP events on the invocation stream; samples rotate and reverse
-the variant order; the median microseconds per decode step is reported.
+times one 16-step generation (the configuration's greedy steps, capacity T = context + 16) with
+HIP events on the invocation stream; samples rotate and reverse the variant order; the median
+microseconds per decode step is reported.
 
-Variants (run.py:24-38): sequential/capture/inferred with reuse off and on, and the 16-step
-batched capture/inferred graphs. "inferred" executes the DAG-derived graph; "capture" is a
-single-stream capture of ordinary launches.
+Variants (run.py:24-38 plus two ablations):
+  sequential / capture / inferred       ordinary launches, single-stream capture, inferred graph
+  branches                              one graph node per dispatch with the reduced DAG's edges
+                                        (the reference's inferred graph: branch concurrency only)
+  contracted                            the inferred graph's contracted and merged launches
+                                        captured on one stream (launch contraction only)
+  *_reuse                               the same with storage reuse on
+  batched_*                             16 steps per graph submission (storage reuse on)
 
-Output: one JSON line on stdout (details per configuration under "configs"); human-readable
-progress on stderr. The CPU baseline (NumPy restatement of the reference decoder step) is timed on
-this host's cores on the same inputs and is also the checker of the measured runs' tokens.
+--steps K is the number of decode steps timed per variant (ceil(K / 16) samples of one 16-step
+generation each); --warmup W the untimed warmup steps per variant. Neither changes the workload.
+
+Output: one JSON line on stdout; progress on stderr. The headline `value` is the large decoder's
+inferred-graph median µs/step (the largest single-GPU configuration of BASELINE.json). The CPU
+baseline (the NumPy restatement of the reference decoder step, oracle/decoder.py) runs in two
+child processes started before any GPU call (all cores, then one thread) from the GPU-prefilled
+state, after the GPU timing; the all-cores run is also the checker of the GPU's tokens and logits.
 """
 from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import platform
+import shutil
 import statistics
+import subprocess
 import sys
+import tempfile
 import time
 from pathlib import Path
 
@@ -35,6 +50,8 @@ import numpy as np  # noqa: E402
 
 HBM_PEAK = 8.0e12          # MI355X HBM3E bytes/s
 METRIC = "median µs/decode step: inferred hipGraph vs stream capture; scratch bytes"
+HEADLINE = "large"
+GENERATION = 16            # greedy steps per generation
 
 
 def log(*parts):
@@ -43,9 +60,10 @@ def log(*parts):
 
 def variants(steps):
     return [("sequential", False, "ordinary", 1), ("capture", False, "capture", 1), ("inferred", False, "graph", 1),
+            ("branches", False, "branches", 1), ("contracted", False, "contracted", 1),
             ("sequential_reuse", True, "ordinary", 1), ("capture_reuse", True, "capture", 1),
             ("inferred_reuse", True, "graph", 1), ("batched_capture", True, "capture", steps),
-            ("batched_inferred", True, "graph", steps)]
+            ("batched_inferred", True, "graph", steps), ("batched_branches", True, "branches", steps)]
 
 
 def algorithmic_step_bytes(c, position):
@@ -115,12 +133,15 @@ def time_variants(session, c, samples, warmup, log_prefix, only=None):
             results.setdefault(name, []).append(timing["wall_us"])
     table = {}
     for name, reuse, mode, group in rows:
-        launches = session.invocations[reuse].launch_count(mode=mode, batch_size=group)
+        inv = session.invocations[reuse]
+        launches = inv.launch_count(mode=mode, batch_size=group)
+        edges = inv.edge_count(mode=mode, batch_size=group)
         table[name] = dict(median_us=statistics.median(metrics[name]), min_us=min(metrics[name]),
                            max_us=max(metrics[name]), wall_us=statistics.median(results[name]),
-                           graph_setup_ms=setup[name], launches_per_submission=launches, steps_per_submission=group,
-                           samples=metrics[name])
-        log(f"{log_prefix} {name:18s} {table[name]['median_us']:9.2f} us/step  launches/submission={launches}")
+                           graph_setup_ms=setup[name], launches_per_submission=launches, graph_edges=edges,
+                           steps_per_submission=group, samples=metrics[name])
+        log(f"{log_prefix} {name:18s} {table[name]['median_us']:9.2f} us/step  launches/submission={launches}"
+            f" edges={edges}")
     return table
 
 
@@ -133,14 +154,14 @@ def run_config(name, c, args, device):
     session.prefill(prompts, mode="ordinary", progress=lambda done, total: log(f"[{name}] prefill {done}/{total}"))
     t2 = time.time()
     log(f"[{name}] inputs+compile+bind {t1 - t0:.1f}s, device prefill of {c.context - 1} steps {t2 - t1:.2f}s")
-    table = time_variants(session, c, args.samples, args.warmup, f"[{name}]", args.variants)
+    table = time_variants(session, c, args.samples, args.warmup_generations, f"[{name}]", args.variants)
     heap = {}
     for reuse, program in session.programs.items():
         heap[str(reuse)] = sum(int(line.split("bytes = ")[1].split(" ")[0]) for line in program.executable_ir.splitlines()
                                if '"ckl_exec.heap"' in line)
-    # State after one timed generation (the checker compares it with the CPU oracle).
+    # State after one 16-step generation from the prefilled state (the CPU checker compares it).
     session.state.reset()
-    session.invocations[True].run(mode="graph" if "batched_inferred" in table else "ordinary", batch_size=c.steps)
+    session.invocations[True].run(mode="graph", batch_size=c.steps)
     final = {k: session.state.download(k) for k in ("tokens", "history", "position", "logits")}
 
     def median(variant):
@@ -151,16 +172,25 @@ def run_config(name, c, args, device):
 
     position = c.context - 1
     mean_bytes = statistics.mean(algorithmic_step_bytes(c, position + s) for s in range(c.steps))
-    step_us = median("batched_inferred") or min(v["median_us"] for v in table.values())
+    step_us = median("inferred") or min(v["median_us"] for v in table.values())
     result = dict(config=vars(c), steps=c.steps, variants=table,
                   inferred_us=median("inferred"), capture_us=median("capture"), ordinary_us=median("sequential"),
+                  branches_us=median("branches"), contracted_us=median("contracted"),
+                  batched_inferred_us=median("batched_inferred"),
                   inferred_over_capture=ratio("capture", "inferred"),
+                  branches_over_capture=ratio("capture", "branches"),
+                  contracted_over_capture=ratio("capture", "contracted"),
+                  inferred_over_contracted=ratio("contracted", "inferred"),
                   inferred_reuse_over_capture_reuse=ratio("capture_reuse", "inferred_reuse"),
+                  batched_branches_over_batched_capture=ratio("batched_capture", "batched_branches"),
                   scratch_bytes={"reuse_off": heap["False"], "reuse_on": heap["True"]},
                   tokens_per_s=c.batch * 1e6 / step_us,
                   algorithmic_bytes_per_step=mean_bytes,
-                  step_hbm_fraction=mean_bytes / (step_us * 1e-6) / HBM_PEAK)
-    log(f"[{name}] inferred/capture speedup {result['inferred_over_capture']}; scratch {heap['False']} -> {heap['True']} B; "
+                  step_hbm_fraction=mean_bytes / (step_us * 1e-6) / HBM_PEAK,
+                  host_planning_ms={"lower": session.lower_ms, "compile_reuse_off": session.compile_ms[False],
+                                    "compile_reuse_on": session.compile_ms[True]})
+    log(f"[{name}] inferred/capture {result['inferred_over_capture']}; branches/capture {result['branches_over_capture']}; "
+        f"contracted/capture {result['contracted_over_capture']}; scratch {heap['False']} -> {heap['True']} B; "
         f"step roofline {result['step_hbm_fraction']:.3f} of 8 TB/s")
     return session, result, final
 
@@ -186,6 +216,9 @@ def unit_family(name):
     itself (chain entry points join their members' names with "__")."""
     name = name[len("ckl_"):] if name.startswith("ckl_") else name
     name = name[:-len("_group")] if name.endswith("_group") else name
+    for suffix in ("_shared2", "_shared3"):
+        name = name[:-len(suffix)] if name.endswith(suffix) else name
+    name = name[:-len("_nt")] if name.endswith("_nt") else name
     return "linear" if name.startswith("linear_") and "__" not in name else name
 
 
@@ -193,10 +226,11 @@ def kernel_roofline(session, c, samples=7):
     """Time every launch of the inferred step (chains contracted, siblings grouped: what the
     headline mode executes) in sequence on the invocation stream, operands as cold as in a graph
     replay: launch k's duration is the difference of the median HIP-event times of the step's
-    first k+1 and first k launches (`samples` repeats each). Returns per-family totals and the roofline entry of the dominant family
-    (largest total time per step): algorithmic bytes per launch / average launch duration. A
-    launch's algorithmic bytes are the sum of its plan nodes' less the hand-offs a chain keeps on
-    chip (the attention chain's scores and probabilities, silu's output, the rotated q and k)."""
+    first k+1 and first k launches (`samples` repeats each). Returns per-family totals and the
+    roofline entry of the dominant family (largest total time per step): algorithmic bytes per
+    launch / average launch duration. A launch's algorithmic bytes are the sum of its plan nodes'
+    less the hand-offs a chain keeps on chip (the attention chain's scores and probabilities,
+    silu's output, the rotated q and k)."""
     inv = session.invocations[False]   # the headline (inferred, storage reuse off) plan
     position = c.context - 1
     nodes = decoder_node_bytes(c, position)
@@ -253,80 +287,229 @@ def kernel_roofline(session, c, samples=7):
     return summary, dominant, roofline
 
 
-def cpu_baseline(session, c, final, threads=None):
-    """NumPy oracle (restatement of the reference's reference.py step) timed on this host, from the
-    same prefilled state; also checks the GPU generation's tokens and logits."""
+# ---------------------------------------------------------------------------- CPU baseline
+def cpu_threads() -> int:
+    """Cores of this process's share: OMP_NUM_THREADS when set (16 on a one-GPU box), else the
+    CPUs it may run on."""
+    value = os.environ.get("OMP_NUM_THREADS", "")
+    return int(value) if value.isdigit() and int(value) > 0 else len(os.sched_getaffinity(0))
+
+
+def cpu_description() -> dict:
+    model = ""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    blas = "unknown"
+    try:
+        deps = np.show_config(mode="dicts")["Build Dependencies"]
+        blas = f"{deps['blas'].get('name')} {deps['blas'].get('version', '')}".strip()
+    except Exception:  # noqa: BLE001 -- numpy builds differ in what show_config reports
+        pass
+    return {"cpu_model": model or platform.processor() or platform.machine(), "nproc": os.cpu_count(),
+            "affinity_cpus": len(os.sched_getaffinity(0)), "numpy": np.__version__, "blas": blas}
+
+
+def start_cpu_workers(directory: Path):
+    """Start the two CPU-baseline processes now, before this process makes any GPU call: one with
+    BLAS/OpenMP threads = this process's cores, one with 1 thread. They wait for the states."""
+    workers = {}
+    for role, threads in (("all", cpu_threads()), ("single", 1)):
+        env = dict(os.environ, OMP_NUM_THREADS=str(threads), OPENBLAS_NUM_THREADS=str(threads),
+                   MKL_NUM_THREADS=str(threads), BLIS_NUM_THREADS=str(threads))
+        workers[role] = (threads, subprocess.Popen([sys.executable, str(Path(__file__).resolve()), "--cpu-worker",
+                                                   str(directory), "--role", role], env=env))
+    return workers
+
+
+def wait_for(path: Path, alive, limit_s: float) -> bool:
+    """Wait until `path` exists; give up when `alive()` turns false or after `limit_s` seconds."""
+    deadline = time.time() + limit_s
+    while time.time() < deadline:
+        if path.exists():
+            return True
+        if not alive():
+            return path.exists()
+        time.sleep(0.2)
+    return False
+
+
+def cpu_worker(directory: Path, role: str) -> None:
+    """Times oracle.decoder.step (the NumPy restatement of the reference's decode step) on the
+    prefilled states the benchmark leaves in `directory`; the "all" role also records the state
+    after one 16-step generation for the benchmark to check the GPU's against."""
     from oracle import decoder as oracle
-    state = session.state
-    initial = {k: (v.copy() if k in oracle.MUTABLE else v) for k, v in state.initial.items()}
-    steps = c.steps
-    times = []
-    reference = None
-    samples = 3 if c.hidden >= 1024 else 7
-    for _ in range(samples):
-        start = time.perf_counter()
-        reference = oracle.expected(initial, c, steps)
-        times.append((time.perf_counter() - start) / steps * 1e6)
-    ok_tokens = np.array_equal(final["history"], reference["history"]) and np.array_equal(final["tokens"], reference["tokens"])
-    logits_err = float(np.max(np.abs(final["logits"] - reference["logits"]) / (np.abs(reference["logits"]) + 1e-6)))
-    close = bool(np.allclose(final["logits"], reference["logits"], atol=2e-5, rtol=3e-4))
-    return dict(value=statistics.median(times), unit="us/step", cores=threads or os.cpu_count(), kind="port",
-                sample=f"{samples} x {steps}-step NumPy generations from the GPU-prefilled state, B={c.batch}",
-                tokens_match=bool(ok_tokens), logits_allclose=close, logits_max_rel_err=logits_err)
+    from programs.decoder_config import Config
+    parent = os.getppid()
+    go = directory / ("go" if role == "all" else "go_single")
+    if not wait_for(go, lambda: os.getppid() == parent, 3 * 3600):
+        return
+    manifest = json.loads(go.read_text())
+    for name in manifest["configs"]:
+        plan = manifest["plan"][name][role]
+        c = Config(**manifest["shapes"][name])
+        folder = directory / name
+        weights = {p.stem: np.load(p, mmap_mode="r") for p in folder.glob("*.npy") if p.stem not in oracle.MUTABLE}
+        times = []
+        for sample in range(plan["samples"]):
+            # Copy-on-write views: each sample starts from the prefilled state without copying it.
+            state = dict(weights, **{k: np.load(folder / f"{k}.npy", mmap_mode="c") for k in oracle.MUTABLE})
+            start = time.perf_counter()
+            for _ in range(plan["steps"]):
+                oracle.step(state, c)
+            times.append((time.perf_counter() - start) / plan["steps"] * 1e6)
+            if role == "all" and sample == 0:
+                np.savez(directory / f"{name}.check.npz", **{k: np.asarray(state[k]) for k in
+                                                              ("tokens", "history", "position", "logits")})
+        (directory / f"{name}.{role}.json").write_text(json.dumps(
+            {"us_per_step": statistics.median(times), "samples": plan["samples"], "steps": plan["steps"], "times": times}))
+    (directory / f"done.{role}").write_text("ok")
 
 
+def save_state(directory: Path, name: str, session) -> None:
+    folder = directory / name
+    folder.mkdir(parents=True, exist_ok=True)
+    for key, value in session.state.initial.items():
+        np.save(folder / f"{key}.npy", np.ascontiguousarray(value))
+
+
+def cpu_baselines(directory: Path, workers, configs: dict, finals: dict) -> dict:
+    """Release the workers (all cores, then one thread), collect timings and check the GPU's final
+    tokens, history, position and logits against the all-cores run's."""
+    from programs.decoder_config import CONFIGS
+    from programs.harness import LOGITS_NORMWISE, normwise_error
+    names = [n for n in configs if (directory / n).exists()]
+    plan = {n: {"all": {"samples": 1 if n == "large" else 7, "steps": GENERATION},
+                "single": {"samples": 1 if n == "large" else 3, "steps": 4 if n == "large" else GENERATION}}
+            for n in names}
+    manifest = json.dumps({"configs": names, "plan": plan, "shapes": {n: vars(CONFIGS[n]) for n in names}})
+    out = {}
+    (directory / "go").write_text(manifest)
+    ok = wait_for(directory / "done.all", lambda: workers["all"][1].poll() is None, 3600)
+    (directory / "go_single").write_text(manifest)
+    ok_single = wait_for(directory / "done.single", lambda: workers["single"][1].poll() is None, 3600)
+    for role, (threads, process) in workers.items():
+        try:
+            process.wait(timeout=60)
+        except subprocess.TimeoutExpired:
+            process.kill()
+    if not ok:
+        log("[cpu] the all-cores CPU baseline did not finish")
+        return out
+    for n in names:
+        row = json.loads((directory / f"{n}.all.json").read_text())
+        check = np.load(directory / f"{n}.check.npz")
+        final = finals[n]
+        tokens = bool(all(np.array_equal(final[k], check[k]) for k in ("tokens", "history", "position")))
+        normwise = normwise_error(final["logits"], check["logits"])
+        entry = {"value": row["us_per_step"], "unit": "us/step", "cores": workers["all"][0], "kind": "port",
+                 "sample": f"{row['samples']} x {row['steps']}-step NumPy generation(s) of oracle/decoder.py from the "
+                           f"GPU-prefilled state, B={CONFIGS[n].batch}",
+                 "tokens_match": tokens, "logits_normwise": normwise, "logits_normwise_ok": normwise <= LOGITS_NORMWISE,
+                 "logits_allclose": bool(np.allclose(final["logits"], check["logits"], atol=2e-5, rtol=3e-4))}
+        if ok_single and (directory / f"{n}.single.json").exists():
+            single = json.loads((directory / f"{n}.single.json").read_text())
+            entry["single_thread"] = {"value": single["us_per_step"], "unit": "us/step", "cores": 1,
+                                      "sample": f"{single['samples']} x {single['steps']}-step generation(s)"}
+        out[n] = entry
+        log(f"[cpu] {n}: {entry}")
+    return out
+
+
+# ---------------------------------------------------------------------------- vector pipeline
 def vector_pipeline(device, samples):
+    """Config V: dst = (src + 0.5) + 0.5 over N = 1,048,576 f32 (examples/vector_pipeline.py),
+    unfused (two `update` launches and one planned 4 MiB temporary, reused across replays) and
+    fused (one generated kernel), in every mode; HBM fraction of the fastest submission."""
     import ckl
     from programs import vector_pipeline as vp
     n = 1048576
-    compiled = {reuse: vp.lower(n).compile(fuse_pointwise=False, reuse_storage=reuse) for reuse in (False, True)}
     spec = ckl.BufferSpec((n,), ckl.f32)
     src, dst = device.empty(spec), device.empty(spec)
     x = np.random.default_rng(123).uniform(-1, 1, n).astype(np.float32)
     src.copy_from_host(x)
-    inv = compiled[True].bind(src, dst, 0.5)
+    expected = (x + np.float32(0.5)) + np.float32(0.5)
     out = {}
-    for mode in ("ordinary", "capture", "graph"):
-        inv.run(mode=mode)
-        got = np.empty_like(x)
-        dst.copy_to_host(got)
-        assert np.array_equal(got, (x + np.float32(0.5)) + np.float32(0.5))
-        inv.benchmark(iterations=20, mode=mode)
-        out[mode] = statistics.median(inv.benchmark(iterations=100, mode=mode)["stream_us"] for _ in range(samples))
-    heap = {str(r): sum(int(l.split("bytes = ")[1].split(" ")[0]) for l in p.executable_ir.splitlines()
-                        if '"ckl_exec.heap"' in l) for r, p in compiled.items()}
-    log(f"[vector_pipeline] us/step {out}; heap {heap}")
-    return dict(us_per_step=out, heap_bytes=heap, bytes_per_step=16 * n)
+    for label, fuse in (("unfused", False), ("fused", True)):
+        compiled = {reuse: vp.lower(n).compile(fuse_pointwise=fuse, reuse_storage=reuse) for reuse in (False, True)}
+        inv = compiled[True].bind(src, dst, 0.5)
+        timing = {}
+        for mode in ("ordinary", "capture", "graph"):
+            inv.run(mode=mode)
+            got = np.empty_like(x)
+            dst.copy_to_host(got)
+            if not np.array_equal(got, expected):
+                raise AssertionError(f"vector_pipeline {label} {mode}: result differs from (src + 0.5) + 0.5")
+            inv.benchmark(iterations=20, mode=mode)
+            runs = [inv.benchmark(iterations=100, mode=mode) for _ in range(samples)]
+            timing[mode] = {"stream_us": statistics.median(r["stream_us"] for r in runs),
+                            "wall_us": statistics.median(r["wall_us"] for r in runs)}
+        heap = {str(r): sum(int(l.split("bytes = ")[1].split(" ")[0]) for l in p.executable_ir.splitlines()
+                            if '"ckl_exec.heap"' in l) for r, p in compiled.items()}
+        traffic = 16 * n if not fuse else 8 * n
+        best = min(v["stream_us"] for v in timing.values())
+        out[label] = dict(us_per_step=timing, heap_bytes=heap, algorithmic_bytes=traffic,
+                          launches=inv.launch_count(mode="ordinary"), hbm_fraction=traffic / (best * 1e-6) / HBM_PEAK)
+        log(f"[vector_pipeline] {label}: {timing}; heap {heap}")
+    return out
 
 
 def main():
     parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     parser.add_argument("--gpus", type=int, default=1)
-    parser.add_argument("--steps", type=int, default=16, help="decode steps per timed generation (config steps)")
-    parser.add_argument("--warmup", type=int, default=3)
-    parser.add_argument("--samples", type=int, default=7)
+    parser.add_argument("--steps", type=int, default=7 * GENERATION,
+                        help="decode steps timed per variant: ceil(steps / 16) samples of one 16-step generation")
+    parser.add_argument("--warmup", type=int, default=3 * GENERATION, help="untimed warmup decode steps per variant")
     parser.add_argument("--seed", type=int, default=123)
     parser.add_argument("--configs", nargs="+", default=["small", "wide", "deep", "large"])
-    parser.add_argument("--variants", nargs="+", default=None, choices=[v[0] for v in variants(16)],
-                        help="time only these variants (default: all); kernel timings and the roofline do "
-                             "not depend on the run mode")
+    parser.add_argument("--variants", nargs="+", default=None, choices=[v[0] for v in variants(GENERATION)],
+                        help="time only these variants (default: all)")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--output", type=Path, default=None, help="also write the full JSON result here")
+    parser.add_argument("--cpu-worker", type=Path, default=None, help=argparse.SUPPRESS)
+    parser.add_argument("--role", default="all", help=argparse.SUPPRESS)
     args = parser.parse_args()
+    if args.cpu_worker:
+        cpu_worker(args.cpu_worker, args.role)
+        return
     if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU: every box here has one MI355X; "
-                          "multi-GPU sharding is a design note (DESIGN.md), not a measured path"}))
+        print(json.dumps({"error": "this build measures one GPU: every box here has one MI355X, and the decode "
+                          "step's sharding over requests or heads is a design note, not a measured path"}))
         sys.exit(2)
-    import dataclasses
+    args.samples = max(1, math.ceil(args.steps / GENERATION))
+    args.warmup_generations = max(0, math.ceil(args.warmup / GENERATION))
+
+    workdir, workers = None, None
+    if not args.no_cpu_baseline:
+        shm = Path("/dev/shm")
+        base = shm if shm.is_dir() and shutil.disk_usage(shm).free > 24 << 30 else None
+        workdir = Path(tempfile.mkdtemp(prefix="ckl_cpu_baseline_", dir=base))
+        workers = start_cpu_workers(workdir)
+    try:
+        line = measure(args, workdir, workers)
+    finally:
+        if workers:
+            for _, process in workers.values():
+                if process.poll() is None:
+                    process.kill()
+        if workdir:
+            shutil.rmtree(workdir, ignore_errors=True)
+    print(json.dumps(line, default=float))
+
+
+def measure(args, workdir, workers):
     import ckl
     from programs.decoder_config import CONFIGS
 
     device = ckl.Device()
     log(f"device: {device.name}")
-    configs = {}
-    headline = None
+    configs, finals = {}, {}
     for name in args.configs:
-        c = dataclasses.replace(CONFIGS[name], steps=args.steps)
+        c = CONFIGS[name]
         session, result, final = run_config(name, c, args, device)
         summary, dominant, roofline = kernel_roofline(session, c)
         result["kernels"] = summary
@@ -339,40 +522,56 @@ def main():
                                          "achieved_GBps": v["achieved_GBps"] if v["avg_us"] > 0 else None,
                                          "frac": v["achieved_GBps"] * 1e9 / HBM_PEAK if v["avg_us"] > 0 else None}
                                      for k, v in summary.items()}
-        if name == "large":
-            result["roofline"] = roofline
-            log(f"[large] dominant kernel {dominant}: {roofline}")
-        if not args.no_cpu_baseline and name in ("small",):
-            result["cpu_baseline"] = cpu_baseline(session, c, final)
-            log(f"[{name}] cpu baseline {result['cpu_baseline']}")
-        configs[name] = result
-        if name == "small":
-            headline = result
+        result["roofline"] = roofline
+        log(f"[{name}] dominant kernel {dominant}: {roofline}")
+        configs[name], finals[name] = result, final
+        if workdir:
+            save_state(workdir, name, session)
         del session
-    vector = vector_pipeline(device, args.samples)
-    head = headline or next(iter(configs.values()))
-    value = next(v for v in (head["inferred_us"], head["ordinary_us"], head["capture_us"]) if v is not None)
-    large = configs.get("large", {})
+    vector = vector_pipeline(device, 7)
+    cpu = cpu_baselines(workdir, workers, configs, finals) if workdir else {}
+    for name, row in cpu.items():
+        configs[name]["cpu_baseline"] = row
+        configs[name]["tokens_match_cpu"] = row["tokens_match"]
+        configs[name]["logits_normwise"] = row["logits_normwise"]
+    headline = HEADLINE if HEADLINE in configs else list(configs)[-1]
+    head = configs[headline]
+    c = CONFIGS[headline]
+    value = head["inferred_us"] if head["inferred_us"] is not None else min(v["median_us"] for v in head["variants"].values())
+    host = cpu_description()
+    baseline = None
+    if headline in cpu:
+        baseline = dict(cpu[headline], **host, planner_ms=head["host_planning_ms"])
+    timed = args.samples * c.steps
     line = {
-        "metric": METRIC, "value": value, "unit": "us/step", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": value / 1000.0, "higher_is_better": False,
-        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic (seeded N(0,0.02) weights, random prompts)",
-        "config": {"workload": "small decoder (B8 C64 A4x16 L2 F256 V256, ctx 16, 16 greedy steps)",
+        "metric": METRIC, "value": value, "unit": "us/step", "n_gpus": 1, "steps": timed,
+        "warmup": args.warmup_generations * c.steps, "ms_per_step": value / 1000.0, "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded N(0,0.02) weights, 1+N(0,0.02) gains, random prompts; GPU teacher-forced prefill)",
+        "config": {"workload": f"{headline} decoder (B{c.batch} C{c.hidden} A{c.heads}x{c.head_dim} L{c.layers} "
+                               f"F{c.ffn} V{c.vocab}, {c.context}-token prompt -> T {c.capacity}, {c.steps} greedy steps)",
                    "inferred_us": head["inferred_us"], "capture_us": head["capture_us"],
-                   "ordinary_us": head["ordinary_us"], "inferred_over_capture": head["inferred_over_capture"],
-                   "scratch_bytes": head["scratch_bytes"], "tokens_per_s": head["tokens_per_s"]},
-        "roofline": large.get("roofline"),
-        "cpu_baseline": head.get("cpu_baseline"),
+                   "ordinary_us": head["ordinary_us"], "branches_us": head["branches_us"],
+                   "contracted_us": head["contracted_us"], "batched_inferred_us": head["batched_inferred_us"],
+                   "inferred_over_capture": head["inferred_over_capture"],
+                   "branches_over_capture": head["branches_over_capture"],
+                   "contracted_over_capture": head["contracted_over_capture"],
+                   "scratch_bytes": head["scratch_bytes"], "tokens_per_s": head["tokens_per_s"],
+                   "step_hbm_fraction": head["step_hbm_fraction"], "logits_normwise": head.get("logits_normwise")},
+        "roofline": head["roofline"],
+        "cpu_baseline": baseline,
         "configs": {k: {kk: vv for kk, vv in v.items() if kk not in ("variants", "kernels")} |
-                    {"variants": {vn: {"median_us": vv["median_us"], "launches": vv["launches_per_submission"]}
+                    {"variants": {vn: {"median_us": vv["median_us"], "launches": vv["launches_per_submission"],
+                                       "edges": vv["graph_edges"], "wall_us": vv["wall_us"],
+                                       "graph_setup_ms": vv["graph_setup_ms"]}
                                   for vn, vv in v["variants"].items()}} for k, v in configs.items()},
         "vector_pipeline": vector,
-        "host": {"cpu": platform.processor() or platform.machine(), "nproc": os.cpu_count(), "numpy": np.__version__},
+        "host": host,
     }
     if args.output:
         full = dict(line, configs_full=configs)
         args.output.write_text(json.dumps(full, indent=1, default=float) + "\n")
-    print(json.dumps(line, default=float))
+    return line
 
 
 if __name__ == "__main__":

@@ -22,7 +22,7 @@ ARCH = os.environ.get("CKL_OFFLOAD_ARCH", "gfx950")
 
 HOST_SOURCES = [
     "core/ir.cpp", "core/planner.cpp", "core/analysis.cpp", "core/fusion.cpp", "core/compiler.cpp",
-    "runtime/runtime.cpp", "runtime/chains.cpp", "runtime/codegen.cpp", "capi.cpp",
+    "runtime/runtime.cpp", "runtime/chains.cpp", "runtime/codegen.cpp", "runtime/kernarg.cpp", "capi.cpp",
 ]
 KERNEL_SOURCES = ["kernels/library.hip"]
 # Packed FP32 instructions are disabled for all device code built here.

@@ -174,12 +174,22 @@ int ckl_program_from_entry(void (*entry)(void **), const uint64_t *bufferBytes, 
                            size_t count, ckl_program *fallback, ckl_program **out) {
   return guarded([&] {
     require(out, "out");
-    if (!entry) throw std::invalid_argument("invalid host entry or argument metadata");
+    // NvidiaProgram's constructor check (lib/Runtime/NvidiaProgram.cpp:136-146): an entry and one
+    // metadata entry per argument. Here each argument is also either a buffer (bytes > 0, no
+    // scalar type) or a scalar of a type bind can pack, so a malformed signature fails now
+    // rather than at every bind.
+    if (!entry || (count && (!bufferBytes || !scalarTypes)))
+      throw std::invalid_argument("invalid host entry or argument metadata");
     auto state = std::make_shared<ckl::rt::ProgramState>();
     state->entry = entry;
     for (size_t k = 0; k < count; ++k) {
-      state->bufferBytes.push_back(bufferBytes ? bufferBytes[k] : 0);
-      state->scalarTypes.push_back(scalarTypes && scalarTypes[k] ? scalarTypes[k] : "");
+      std::string type = scalarTypes[k] ? scalarTypes[k] : "";
+      bool scalar = type == "i32" || type == "i64" || type == "f32" || type == "f64";
+      if (bufferBytes[k] ? !type.empty() : !scalar)
+        throw std::invalid_argument("invalid host entry or argument metadata: argument " + std::to_string(k) +
+                                    " must be a buffer with a byte size or an i32/i64/f32/f64 scalar");
+      state->bufferBytes.push_back(bufferBytes[k]);
+      state->scalarTypes.push_back(type);
     }
     if (fallback) state->aliasFallback = fallback->state;
     *out = new ckl_program{nullptr, state};
@@ -352,6 +362,33 @@ int ckl_invocation_launch_count(ckl_invocation *invocation, int mode, uint64_t b
     require(invocation, "invocation");
     require(count, "count");
     *count = invocation->invocation->graphNodeCount(mode, batch);
+  });
+}
+
+int ckl_invocation_edge_count(ckl_invocation *invocation, int mode, uint64_t batch, uint64_t *count) {
+  return guarded([&] {
+    require(invocation, "invocation");
+    require(count, "count");
+    *count = invocation->invocation->graphEdgeCount(mode, batch);
+  });
+}
+
+int ckl_code_object_arguments(const void *image, uint64_t bytes, const char *kernel, uint32_t *offsets,
+                              uint32_t *sizes, uint64_t capacity, uint64_t *count, uint32_t *segment_bytes) {
+  return guarded([&] {
+    require(image, "image");
+    require(kernel, "kernel");
+    require(count, "count");
+    auto table = ckl::rt::readKernelSignatures(image, bytes);
+    auto found = table.find(kernel);
+    if (found == table.end()) throw std::invalid_argument(std::string("code object has no kernel ") + kernel);
+    const auto &args = found->second.arguments;
+    *count = args.size();
+    for (size_t k = 0; k < args.size() && k < capacity; ++k) {
+      if (offsets) offsets[k] = args[k].offset;
+      if (sizes) sizes[k] = args[k].size;
+    }
+    if (segment_bytes) *segment_bytes = found->second.segmentBytes;
   });
 }
 

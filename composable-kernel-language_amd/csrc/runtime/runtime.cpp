@@ -23,11 +23,6 @@ bool inferredOnStream() {
   return value && std::strcmp(value, "1") == 0;
 }
 
-BranchPolicy branchPolicy() {
-  const char *value = std::getenv("CKL_GRAPH_BRANCHES");
-  return value && std::strcmp(value, "1") == 0 ? BranchPolicy::Branches : BranchPolicy::Grouped;
-}
-
 // ====================================================================== device and buffers
 static std::atomic<uint64_t> nextDeviceId{0};
 
@@ -52,11 +47,24 @@ hipModule_t Device::load(const std::string &identity, const void *image, size_t 
   auto found = modules.find(identity);
   if (found != modules.end()) return found->second;
   if (!image || !bytes) throw std::invalid_argument("cannot load an empty code object");
+  std::map<std::string, KernelSignature> layouts = readKernelSignatures(image, bytes);
   makeCurrent();
   hipModule_t module = nullptr;
   check(hipModuleLoadData(&module, image), "hipModuleLoadData");
+  for (auto &[name, layout] : layouts) {
+    hipFunction_t function = nullptr;
+    if (hipModuleGetFunction(&function, module, name.c_str()) == hipSuccess) signatures[function] = std::move(layout);
+    else (void)hipGetLastError();
+  }
   modules[identity] = module;
   return module;
+}
+
+const KernelSignature &Device::signature(hipFunction_t function) {
+  std::lock_guard<std::mutex> lock(moduleMutex);
+  auto found = signatures.find(function);
+  if (found == signatures.end()) throw std::logic_error("kernel function has no argument layout in its code object");
+  return found->second;
 }
 
 void Buffer::copyFromHost(const void *data, uint64_t size) const {
@@ -147,6 +155,43 @@ GraphExec::~GraphExec() {
   if (graph) hipGraphDestroy(graph);
 }
 
+void prepareParams(Launch &launch, Device &device) {
+  const KernelSignature &layout = device.signature(launch.function);
+  const std::vector<KernelArgument> &args = layout.arguments;
+  const size_t have = launch.arguments.size();
+  auto mismatch = [&](const std::string &why) {
+    return std::invalid_argument("argument block of kernel " + launch.name + " (" + std::to_string(have) +
+                                 " bytes) does not match its code object's declared arguments: " + why);
+  };
+  launch.paramOffsets.clear();
+  launch.prepared = false;
+  if (args.empty()) {
+    if (!launch.slotOffsets.empty()) throw mismatch("the kernel takes no arguments");
+    launch.prepared = true;
+    return;
+  }
+  if (args.size() == 1 && args[0].offset == 0) {
+    // One argument (a struct of the packed fields, or a single field): HIP copies args[0].size
+    // bytes from the block; the block is that many bytes plus the 8-byte padding of the packer.
+    if (have < args[0].size || have - args[0].size >= 8)
+      throw mismatch("one argument of " + std::to_string(args[0].size) + " bytes");
+    launch.paramOffsets.push_back(0);
+    launch.prepared = true;
+    return;
+  }
+  if (launch.slotOffsets.size() != args.size() || launch.slotSizes.size() != args.size())
+    throw mismatch(std::to_string(args.size()) + " arguments, " + std::to_string(launch.slotOffsets.size()) + " packed");
+  for (size_t k = 0; k < args.size(); ++k) {
+    if (launch.slotOffsets[k] != args[k].offset || launch.slotSizes[k] != args[k].size)
+      throw mismatch("argument " + std::to_string(k) + " is " + std::to_string(args[k].size) + " bytes at offset " +
+                     std::to_string(args[k].offset) + ", packed " + std::to_string(launch.slotSizes[k]) +
+                     " bytes at offset " + std::to_string(launch.slotOffsets[k]));
+    if (size_t(args[k].offset) + args[k].size > have) throw mismatch("argument " + std::to_string(k) + " past the block");
+    launch.paramOffsets.push_back(args[k].offset);
+  }
+  launch.prepared = true;
+}
+
 void bindVariants(Launch &launch, const std::string &entry) {
   launch.groupFunction = nullptr;
   launch.sharedFunction[0] = launch.sharedFunction[1] = nullptr;
@@ -165,10 +210,23 @@ namespace {
 
 constexpr size_t kMaxGroup = 4;
 
+// hipModuleLaunchKernel reads explicit argument i from params[i] with the size the code object
+// declares; Invocation::prepare has checked that `arguments` holds every one of them.
+constexpr size_t kMaxParams = 64;
+
+struct Params {
+  void *at[kMaxParams] = {};
+  Params(const Launch &launch, const uint8_t *block) {
+    if (!launch.prepared || launch.paramOffsets.size() > kMaxParams)
+      throw std::logic_error("launch " + launch.name + " has no prepared argument layout");
+    for (size_t k = 0; k < launch.paramOffsets.size(); ++k) at[k] = const_cast<uint8_t *>(block + launch.paramOffsets[k]);
+  }
+};
+
 void launchOne(const Launch &launch, hipStream_t stream) {
-  void *params[] = {const_cast<uint8_t *>(launch.arguments.data())};
+  Params params(launch, launch.arguments.data());
   check(hipModuleLaunchKernel(launch.function, launch.grid[0], launch.grid[1], launch.grid[2], launch.block[0],
-                              launch.block[1], launch.block[2], launch.shared, stream, params, nullptr),
+                              launch.block[1], launch.block[2], launch.shared, stream, params.at, nullptr),
         "hipModuleLaunchKernel");
 }
 
@@ -312,10 +370,10 @@ std::unique_ptr<GraphExec> captureUnits(const std::vector<Launch> &launches, hip
   check(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
   try {
     for (size_t k = 0; k < launches.size(); ++k) {
-      void *params[] = {out->storage[k].data()};
       const Launch &l = launches[k];
+      Params params(l, out->storage[k].data());
       check(hipModuleLaunchKernel(l.function, l.grid[0], l.grid[1], l.grid[2], l.block[0], l.block[1], l.block[2],
-                                  l.shared, stream, params, nullptr),
+                                  l.shared, stream, params.at, nullptr),
             "hipModuleLaunchKernel(capture)");
     }
   } catch (...) {
@@ -332,33 +390,60 @@ std::unique_ptr<GraphExec> captureUnits(const std::vector<Launch> &launches, hip
   return out;
 }
 
-// Explicit graph with one kernel node per unit and the units' dependency edges.
+// Explicit graph with one kernel node per unit and the units' dependency edges, transitively
+// reduced at unit level (contracting chains and merging siblings can make plan edges redundant).
 std::unique_ptr<GraphExec> explicitGraph(const Plan &plan, const std::vector<Unit> &units) {
   auto out = std::make_unique<GraphExec>();
+  const size_t n = units.size();
   std::vector<size_t> unitOf(plan.nodes.size());
-  for (size_t u = 0; u < units.size(); ++u) for (size_t m : units[u].members) unitOf[m] = u;
-  check(hipGraphCreate(&out->graph, 0), "hipGraphCreate");
-  std::vector<hipGraphNode_t> handles(units.size());
-  for (const Unit &u : units) out->storage.push_back(u.launch.arguments);
-  for (size_t u = 0; u < units.size(); ++u) {
-    std::vector<hipGraphNode_t> deps;
-    std::vector<size_t> seen;
+  for (size_t u = 0; u < n; ++u) for (size_t m : units[u].members) unitOf[m] = u;
+  // Units arrive in a topological order (groupPlan levels them; one node per dispatch keeps plan
+  // order), so every edge goes from a lower to a higher unit index.
+  std::vector<std::vector<size_t>> preds(n);
+  for (size_t u = 0; u < n; ++u) {
     for (size_t m : units[u].members)
       for (size_t d : plan.nodes[m].dependencies) {
         size_t du = unitOf[d];
-        if (du != u && std::find(seen.begin(), seen.end(), du) == seen.end()) { seen.push_back(du); deps.push_back(handles[du]); }
+        if (du == u) continue;
+        if (du > u) throw std::logic_error("inferred graph units are not in topological order");
+        preds[u].push_back(du);
       }
+    std::sort(preds[u].begin(), preds[u].end());
+    preds[u].erase(std::unique(preds[u].begin(), preds[u].end()), preds[u].end());
+  }
+  // reach[u]: units that u depends on, directly or not (bit sets over unit indices).
+  const size_t words = (n + 63) / 64;
+  std::vector<uint64_t> reach(n * words, 0);
+  std::vector<std::vector<size_t>> reduced(n);
+  for (size_t u = 0; u < n; ++u) {
+    uint64_t *mine = &reach[u * words];
+    // A predecessor is kept when no later predecessor already reaches it (scan in descending order).
+    for (auto it = preds[u].rbegin(); it != preds[u].rend(); ++it) {
+      size_t p = *it;
+      if (!(mine[p / 64] >> (p % 64) & 1)) reduced[u].push_back(p);
+      mine[p / 64] |= uint64_t(1) << (p % 64);
+      const uint64_t *theirs = &reach[p * words];
+      for (size_t w = 0; w < words; ++w) mine[w] |= theirs[w];
+    }
+  }
+  check(hipGraphCreate(&out->graph, 0), "hipGraphCreate");
+  std::vector<hipGraphNode_t> handles(n);
+  for (const Unit &u : units) out->storage.push_back(u.launch.arguments);
+  for (size_t u = 0; u < n; ++u) {
+    std::vector<hipGraphNode_t> deps;
+    for (size_t p : reduced[u]) deps.push_back(handles[p]);
     const Launch &l = units[u].launch;
-    void *params[] = {out->storage[u].data()};
+    Params params(l, out->storage[u].data());
     hipKernelNodeParams p{};
     p.func = reinterpret_cast<void *>(l.function);
     p.gridDim = dim3(l.grid[0], l.grid[1], l.grid[2]);
     p.blockDim = dim3(l.block[0], l.block[1], l.block[2]);
     p.sharedMemBytes = l.shared;
-    p.kernelParams = params;
+    p.kernelParams = params.at;
     check(hipGraphAddKernelNode(&handles[u], out->graph, deps.data(), deps.size(), &p), "hipGraphAddKernelNode");
+    out->edgeCount += deps.size();
   }
-  out->nodeCount = units.size();
+  out->nodeCount = n;
   check(hipGraphInstantiate(&out->exec, out->graph, nullptr, nullptr, 0), "hipGraphInstantiate");
   return out;
 }
@@ -382,7 +467,8 @@ Invocation::~Invocation() {
 }
 
 void Invocation::validate(int mode, uint64_t batch) const {
-  if (mode < 0 || mode > 2 || !batch || plan.nodes.empty() || batch > 1000000 / plan.nodes.size())
+  if (mode < kOrdinary || mode > kContractedCapture || !batch || plan.nodes.empty() ||
+      batch > 1000000 / plan.nodes.size())
     throw std::invalid_argument("invalid execution mode or batch exceeds one million kernel nodes");
 }
 
@@ -390,22 +476,25 @@ GraphExec &Invocation::graphFor(int mode, uint64_t batch) {
   auto &slot = graphs[{mode, batch}];
   if (!slot) {
     Plan repeated = batch == 1 ? plan : plan.repeat(batch);
-    if (mode == 2) {
+    if (mode == kCapture) {
       std::vector<Launch> launches;
       for (const PlanNode &n : repeated.nodes) launches.push_back(n.launch);
       slot = captureUnits(launches, stream);
-    } else if (branchPolicy() == BranchPolicy::Branches) {
+    } else if (mode == kBranches) {
+      // The reference's inferred graph: one kernel node per dispatch, reduced DAG edges.
       std::vector<Unit> units;
       for (size_t k = 0; k < repeated.nodes.size(); ++k) units.push_back({{k}, repeated.nodes[k].launch});
       slot = explicitGraph(repeated, units);
     } else {
-      // Chains contracted, sibling groups ordered by DAG level, captured as one launch chain.
+      // Chains contracted, siblings of one family merged, units levelled by DAG depth; mode 1
+      // keeps the units' DAG as an explicit graph, mode 4 captures them as one launch chain.
       std::vector<Chain> chains = findChains(plan, temporaryResources);
       std::map<size_t, Launch> deferred = deferCombines(plan, temporaryResources, chains);
       std::vector<Unit> units = groupPlan(repeated, chains, deferred, batch);
+      for (Unit &u : units) prepareParams(u.launch, *device);
       std::vector<Launch> launches;
       for (const Unit &u : units) launches.push_back(u.launch);
-      slot = captureUnits(launches, stream);
+      slot = mode == kInferred ? explicitGraph(repeated, units) : captureUnits(launches, stream);
       slot->launches = std::move(launches);
       for (Unit &u : units) slot->members.push_back(std::move(u.members));
     }
@@ -415,22 +504,29 @@ GraphExec &Invocation::graphFor(int mode, uint64_t batch) {
 
 void Invocation::execute(int mode, uint64_t batch) {
   device->makeCurrent();
-  if (mode) {
-    GraphExec &graph = graphFor(mode, batch);
-    if (mode == 1 && !graph.launches.empty() && inferredOnStream())
-      for (const Launch &l : graph.launches) launchOne(l, stream);
-    else
-      check(hipGraphLaunch(graph.exec, stream), "hipGraphLaunch");
-  } else {
+  if (mode == kOrdinary) {
     for (uint64_t k = 0; k < batch; ++k) launchOrdinary(plan, stream);
+    return;
   }
+  GraphExec &graph = graphFor(mode, batch);
+  if ((mode == kInferred || mode == kContractedCapture) && !graph.launches.empty() && inferredOnStream())
+    for (const Launch &l : graph.launches) launchOne(l, stream);
+  else
+    check(hipGraphLaunch(graph.exec, stream), "hipGraphLaunch");
 }
 
 size_t Invocation::graphNodeCount(int mode, uint64_t batch) {
   std::lock_guard<std::mutex> lock(runMutex);
   validate(mode, batch);
-  if (!mode) return plan.nodes.size() * batch;
+  if (mode == kOrdinary) return plan.nodes.size() * batch;
   return graphFor(mode, batch).nodeCount;
+}
+
+size_t Invocation::graphEdgeCount(int mode, uint64_t batch) {
+  std::lock_guard<std::mutex> lock(runMutex);
+  validate(mode, batch);
+  if (mode == kOrdinary) return 0;
+  return graphFor(mode, batch).edgeCount;
 }
 
 void Invocation::run(int mode, uint64_t batch) {
@@ -481,10 +577,8 @@ double Invocation::timeNode(size_t index, uint64_t iterations) {
 }
 
 GraphExec &Invocation::inferredUnits() {
-  if (branchPolicy() != BranchPolicy::Grouped)
-    throw std::invalid_argument("inferred units are defined for the grouped graph policy only");
-  validate(1, 1);
-  return graphFor(1, 1);
+  validate(kInferred, 1);
+  return graphFor(kInferred, 1);
 }
 
 size_t Invocation::unitCount() {
@@ -591,6 +685,7 @@ static void appendArgument(Launch &launch, const void *data, uint64_t size, int6
   launch.arguments.resize(offset + size, 0);
   std::memcpy(launch.arguments.data() + offset, data, size);
   launch.slotOffsets.push_back(offset);
+  launch.slotSizes.push_back(size);
   launch.slotResources.push_back(resource);
 }
 
@@ -744,6 +839,7 @@ extern "C" void ckl_commit(void *frame, uint64_t id) {
         (void)hipGetLastError();
       }
     }
+    ckl::rt::prepareParams(f.pending, *f.device);
     f.nodes[id] = f.plan.addKernel(std::move(f.pending), std::move(f.dependencies));
     f.pending = Launch();
     f.dependencies.clear();

@@ -5,10 +5,14 @@
 //   lib/Runtime/NvidiaProgram.cpp:13-294    callback ABI, bind, run, benchmark
 //   lib/Runtime/HipRuntime.cpp:212-466      hipModule loading and kernel nodes
 // Execution modes: 0 ordinary launches, 1 inferred graph (from the plan's dependency DAG),
-// 2 single-stream capture of ordinary launches.
+// 2 single-stream capture of ordinary launches (the reference's three, NvidiaProgram.cpp:115-131),
+// and two ablations of mode 1: 3 the reference's own inferred graph (one kernel node per dispatch
+// with the reduced DAG's edges, NvidiaRuntime.cpp:391-433) and 4 mode 1's contracted launches
+// captured on one stream in level order (no graph branches).
 #pragma once
 
 #include "callbacks.h"
+#include "kernarg.h"
 
 #include <hip/hip_runtime.h>
 
@@ -25,6 +29,8 @@ namespace ckl::rt {
 
 void check(hipError_t status, const char *what);
 
+enum Mode { kOrdinary = 0, kInferred = 1, kCapture = 2, kBranches = 3, kContractedCapture = 4 };
+
 struct Device {
   explicit Device(int ordinal);
   ~Device();
@@ -33,7 +39,11 @@ struct Device {
   std::string name;
   std::mutex moduleMutex;
   std::map<std::string, hipModule_t> modules;   // artifact identity -> loaded module
+  // Explicit argument layout of every kernel of every loaded module (from its metadata note).
+  std::map<hipFunction_t, KernelSignature> signatures;
   hipModule_t load(const std::string &identity, const void *image, size_t bytes);
+  // Layout of a kernel of a module loaded here; throws std::logic_error for an unknown function.
+  const KernelSignature &signature(hipFunction_t function);
   void makeCurrent() const;
 };
 
@@ -64,7 +74,12 @@ struct Launch {
   unsigned block[3] = {1, 1, 1};
   unsigned shared = 0;
   std::vector<uint8_t> arguments;           // kernarg bytes (natural alignment, padded to 8)
+  // Where each explicit kernel argument starts in `arguments` (from the code object's metadata;
+  // set by Invocation::prepare before the launch is issued or recorded).
+  std::vector<uint32_t> paramOffsets;
+  bool prepared = false;
   std::vector<size_t> slotOffsets;
+  std::vector<size_t> slotSizes;
   std::vector<int64_t> slotResources;       // per slot: the plan resource it addresses, or -1
 };
 
@@ -103,13 +118,17 @@ bool sharesOperands(const std::vector<const Launch *> &members);
 bool streams(const Launch &launch);
 // Looks up the _group and _shared<M> entry points of `entry` in the launch's module.
 void bindVariants(Launch &launch, const std::string &entry);
+// Checks the launch's packed block against the explicit arguments its code object declares for
+// `launch.function` and records where each argument starts (std::invalid_argument on mismatch).
+void prepareParams(Launch &launch, Device &device);
 
 struct GraphExec {
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
   size_t nodeCount = 0;
+  size_t edgeCount = 0;                        // dependency edges of an explicit graph
   std::vector<std::vector<uint8_t>> storage;   // kernarg blocks referenced during capture
-  std::vector<Launch> launches;                // the captured launch chain (grouped inferred policy)
+  std::vector<Launch> launches;                // contracted units in level order (modes 1 and 4)
   std::vector<std::vector<size_t>> members;    // plan nodes each of those launches executes
   ~GraphExec();
 };
@@ -141,6 +160,7 @@ struct Invocation {
   std::array<double, 3> benchmark(int mode, uint64_t iterations, uint64_t batch);
   size_t nodeCount() const { return plan.nodes.size(); }
   size_t graphNodeCount(int mode, uint64_t batch);
+  size_t graphEdgeCount(int mode, uint64_t batch);
   // Average duration (us) of plan node `index` launched `iterations` times back to back on the
   // invocation stream, bracketed by HIP events.
   double timeNode(size_t index, uint64_t iterations);
@@ -188,12 +208,7 @@ struct Argument {
 std::shared_ptr<Invocation> bind(const std::shared_ptr<ProgramState> &program, std::shared_ptr<Device> device,
                                  const std::vector<Argument> &arguments);
 
-// Graph policy for mode 1: contract library chains, group sibling dispatches of one library
-// family into one launch and capture the result as one launch chain (default), or keep one graph
-// node per dispatch with real branches.
-enum class BranchPolicy { Grouped, Branches };
-BranchPolicy branchPolicy();
-// CKL_INFERRED_STREAM=1: mode 1 issues the grouped inferred launch chain as ordinary stream
+// CKL_INFERRED_STREAM=1: modes 1 and 4 issue the contracted launch chain as ordinary stream
 // launches instead of one graph launch (same kernels and order; for per-kernel profiling).
 bool inferredOnStream();
 

@@ -7,8 +7,6 @@ from __future__ import annotations
 
 from dataclasses import dataclass
 
-import ckl
-
 
 @dataclass(frozen=True)
 class Config:
@@ -60,6 +58,7 @@ def shapes(c: Config) -> dict:
 
 
 def signature(c: Config) -> dict:
+    import ckl
     types = {"i32": ckl.i32, "f32": ckl.f32}
     sig = {name: ckl.BufferSpec(shape, types[dtype]) for name, (shape, dtype) in shapes(c).items()}
     sig.update(epsilon=ckl.f32, attention_scale=ckl.f32)

@@ -75,6 +75,11 @@ _SIGNATURES = {
     "ckl_invocation_node_count": ([ctypes.c_void_p], ctypes.c_uint64),
     "ckl_invocation_launch_count": ([ctypes.c_void_p, ctypes.c_int, ctypes.c_uint64, ctypes.POINTER(ctypes.c_uint64)],
                                     ctypes.c_int),
+    "ckl_invocation_edge_count": ([ctypes.c_void_p, ctypes.c_int, ctypes.c_uint64, ctypes.POINTER(ctypes.c_uint64)],
+                                  ctypes.c_int),
+    "ckl_code_object_arguments": ([ctypes.c_void_p, ctypes.c_uint64, ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint32),
+                                   ctypes.POINTER(ctypes.c_uint32), ctypes.c_uint64, ctypes.POINTER(ctypes.c_uint64),
+                                   ctypes.POINTER(ctypes.c_uint32)], ctypes.c_int),
     "ckl_invocation_time_node": ([ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint64, ctypes.POINTER(ctypes.c_double)],
                                  ctypes.c_int),
     "ckl_invocation_node_name": ([ctypes.c_void_p, ctypes.c_uint64], ctypes.c_char_p),

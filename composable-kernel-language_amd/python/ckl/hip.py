@@ -268,7 +268,10 @@ class CompiledProgram(_ContextManager):
 class Invocation(_ContextManager):
     """A bound program: one stream, its planned heaps and cached graphs."""
 
-    MODES = {"ordinary": 0, "graph": 1, "capture": 2}
+    # The reference's three modes, plus two ablations of the inferred graph: "branches" is one
+    # graph node per dispatch with the reduced DAG's edges (the reference's inferred graph) and
+    # "contracted" captures the inferred graph's contracted launches on one stream.
+    MODES = {"ordinary": 0, "graph": 1, "capture": 2, "branches": 3, "contracted": 4}
 
     def __init__(self, program, device, arguments, resource: _Handle):
         self.program, self.device, self.arguments = program, device, arguments
@@ -285,7 +288,7 @@ class Invocation(_ContextManager):
         if mode is not None and graph:
             raise ValueError("specify either graph or mode")
         if mode is not None and mode not in cls.MODES:
-            raise ValueError("mode must be ordinary, graph, or capture")
+            raise ValueError("mode must be ordinary, graph, capture, branches, or contracted")
         return cls.MODES[mode] if mode is not None else int(bool(graph))
 
     def run(self, *, graph=False, mode=None, batch_size=1) -> "Invocation":
@@ -302,6 +305,13 @@ class Invocation(_ContextManager):
         """Device launches one execution submits (graph nodes for graph modes)."""
         count = ctypes.c_uint64()
         _native.check(_native.native().ckl_invocation_launch_count(
+            self._native_resource.pointer, self._execution(False, mode, batch_size), batch_size, ctypes.byref(count)))
+        return int(count.value)
+
+    def edge_count(self, *, mode="graph", batch_size=1) -> int:
+        """Dependency edges of the explicit graph of `mode` ("graph" or "branches"; 0 otherwise)."""
+        count = ctypes.c_uint64()
+        _native.check(_native.native().ckl_invocation_edge_count(
             self._native_resource.pointer, self._execution(False, mode, batch_size), batch_size, ctypes.byref(count)))
         return int(count.value)
 

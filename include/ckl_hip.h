@@ -94,6 +94,15 @@ int ckl_plan_storage(size_t node_count, const uint64_t *edges, size_t edge_count
                      size_t resource_count, int reuse_storage, uint64_t *baseline_bytes, uint64_t *planned_bytes,
                      ckl_storage_assignment *out);
 
+/* Explicit arguments of `kernel` as its gfx950 code object declares them (the AMDGPU metadata
+ * note of an ELF code object or of the gfx950 entry of an offload bundle): up to `capacity`
+ * offsets and sizes, their number in *count and the kernarg segment size (explicit + hidden) in
+ * *segment_bytes. No reference counterpart: the executor checks every packed argument block
+ * against this layout before a launch (CUDA's driver sizes a packed block itself), and tools
+ * can inspect it. */
+int ckl_code_object_arguments(const void *image, uint64_t bytes, const char *kernel, uint32_t *offsets,
+                              uint32_t *sizes, uint64_t capacity, uint64_t *count, uint32_t *segment_bytes);
+
 /* Identity of the hand-written gfx950 kernel library code object ("" when absent). */
 const char *ckl_library_identity(void);
 
@@ -129,7 +138,12 @@ typedef struct {
  * invocation (one stream, one allocation per planned heap). */
 int ckl_bind(ckl_program *program, ckl_device *device, const ckl_argument *arguments, size_t count,
              ckl_invocation **out);
-/* mode: 0 ordinary launches, 1 inferred graph, 2 single-stream capture (NvidiaProgram.h:327-330).
+/* mode: 0 ordinary launches, 1 inferred graph, 2 single-stream capture (the reference's three,
+ * lib/Runtime/NvidiaProgram.cpp:115-131), plus two ablations of mode 1 with no reference
+ * counterpart as separate modes: 3 one kernel node per dispatch with the reduced DAG's edges (the
+ * reference's own inferred graph, lib/Runtime/NvidiaRuntime.cpp:391-433: branch concurrency
+ * only) and 4 mode 1's contracted and merged launches captured on one stream (contraction only).
+ * Mode 1 is those contracted launches as an explicit graph with their DAG edges.
  * Synchronizes the invocation stream before returning. */
 int ckl_invocation_run(ckl_invocation *invocation, int mode, uint64_t batch);
 /* out[0] stream us/step, out[1] wall us/step, out[2] graph setup ms (NvidiaProgram.cpp:225-270). */
@@ -137,6 +151,9 @@ int ckl_invocation_benchmark(ckl_invocation *invocation, int mode, uint64_t iter
 uint64_t ckl_invocation_node_count(ckl_invocation *invocation);
 /* Number of device launches (graph nodes) one execution of `batch` steps submits in `mode`. */
 int ckl_invocation_launch_count(ckl_invocation *invocation, int mode, uint64_t batch, uint64_t *count);
+/* Dependency edges of the explicit graph of `mode` (1 or 3; 0 for the other modes, whose
+ * launches are ordered by the stream). No reference counterpart: reports the graph's shape. */
+int ckl_invocation_edge_count(ckl_invocation *invocation, int mode, uint64_t batch, uint64_t *count);
 /* Kernel-level timing for roofline measurement (no reference counterpart; the reference profiles
  * with nsys): plan node `index` (0 .. node_count-1, executable-plan order) is launched
  * `iterations` times back to back on the invocation stream between two HIP events; the average
