@@ -4,7 +4,7 @@ Public names follow python/ckl/__init__.py:1-27 of the reference (the NVIDIA tar
 replaced by AMDTarget).
 """
 from .compiler import AMDTarget, CompilationError, CompiledModule, compile_module
-from .frontend import FrontendError, LoweredProgram, kernel, program
+from .frontend import FrontendError, LoweredProgram, block, kernel, program
 from .frontend.source import INTRINSICS as _intrinsics
 from .hip import CompiledProgram, Device, DeviceBuffer, Invocation, runtime_available
 from .types import Buffer, BufferSpec, constexpr, dim, f32, f64, i32, i64, index
@@ -16,5 +16,5 @@ __all__ = [
     "AMDTarget", "CompilationError", "CompiledModule", "compile_module",
     "CompiledProgram", "Device", "DeviceBuffer", "Invocation", "runtime_available",
     "Buffer", "BufferSpec", "constexpr", "dim", "f32", "f64", "i32", "i64", "index", "bool",
-    "FrontendError", "LoweredProgram", "kernel", "program", *_intrinsics,
+    "FrontendError", "LoweredProgram", "block", "kernel", "program", *_intrinsics,
 ]

@@ -1,4 +1,4 @@
 from .emitter import LoweredProgram
-from .source import FrontendError, INTRINSICS, kernel, program
+from .source import INTRINSICS, FrontendError, block, kernel, program
 
-__all__ = ["FrontendError", "LoweredProgram", "kernel", "program"]
+__all__ = ["FrontendError", "LoweredProgram", "block", "kernel", "program"]

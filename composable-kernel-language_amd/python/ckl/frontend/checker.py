@@ -1,8 +1,10 @@
-"""Resolve annotations and bind a concrete specialization (shapes, dtypes, constants).
+"""Specialisation: resolve a definition's annotations and bind them to a concrete signature.
 
-Rules follow python/ckl/frontend/checker.py:17-142 of the reference: annotations may be CKL
-types or strings naming them; dimension names unify across buffer parameters; constexpr
-parameters bind only through `constants`.
+A specialisation fixes every runtime parameter to a BufferSpec or a numeric scalar type and every
+`constexpr` parameter to a Python constant that fits its type. Dimensions named in buffer
+annotations are unified across parameters (one size per name). The rules and diagnostics are the
+reference's (python/ckl/frontend/checker.py:17-142); the implementation is a small binder over
+the captured annotations.
 """
 from __future__ import annotations
 
@@ -17,61 +19,94 @@ from ..types import (Buffer, BufferSpec, BufferType, ConstexprType, Dimension, N
 from .source import Definition, Namespace, UnsupportedBinding
 
 
-def resolve(node: ast.AST, definition: Definition) -> object:
-    if isinstance(node, ast.Constant) and type(node.value) in (str, int, float, bool, type(None)):
-        if isinstance(node.value, str):
-            return resolve(ast.parse(node.value, mode="eval").body, definition)
-        return node.value
-    if isinstance(node, ast.Name):
+# ------------------------------------------------------------------------- annotations
+def resolve(node: ast.AST, definition: Definition):
+    """Evaluate an annotation expression against the definition's captured names."""
+    if isinstance(node, ast.Constant):
+        value = node.value
+        if isinstance(value, str):             # a string annotation is parsed and evaluated
+            return resolve(ast.parse(value, mode="eval").body, definition)
+        if type(value) in (int, float, bool) or value is None:
+            return value
+    elif isinstance(node, ast.Name):
         if node.id not in definition.bindings:
             raise definition.error(node, f"unknown captured name '{node.id}'")
         value = definition.bindings[node.id]
         if isinstance(value, UnsupportedBinding):
             raise definition.error(node, f"unsupported captured binding '{node.id}'")
         return value
-    if isinstance(node, ast.Attribute):
-        base = resolve(node.value, definition)
-        if isinstance(base, Namespace) and node.attr in base.values:
-            return base.values[node.attr]
-    if isinstance(node, ast.Tuple):
+    elif isinstance(node, ast.Attribute):
+        namespace = resolve(node.value, definition)
+        if isinstance(namespace, Namespace) and node.attr in namespace.values:
+            return namespace.values[node.attr]
+    elif isinstance(node, ast.Tuple):
         return tuple(resolve(item, definition) for item in node.elts)
-    if isinstance(node, ast.Subscript):
-        base = resolve(node.value, definition)
-        arguments = resolve(node.slice, definition)
-        try:
-            if base is Buffer:
-                return Buffer[arguments]
-            if base is constexpr:
-                return constexpr[arguments]
-        except ValueError as error:
-            raise definition.error(node, str(error)) from error
+    elif isinstance(node, ast.Subscript):
+        constructor = resolve(node.value, definition)
+        if constructor is Buffer or constructor is constexpr:
+            try:
+                return constructor[resolve(node.slice, definition)]
+            except ValueError as error:
+                raise definition.error(node, str(error)) from error
     raise definition.error(node, "unsupported annotation; use CKL types and shape declarations")
 
 
-def constant(value: object, dtype: ScalarType, definition: Definition, node: ast.AST) -> object:
-    """Check that a Python constant fits `dtype`; f32 values are rounded to f32."""
+def annotation_of(definition: Definition, argument: ast.arg):
+    """The CKL type of one parameter: the captured annotation object, or its source expression."""
+    captured = definition.annotations.get(argument.arg)
+    if captured is not None and not isinstance(captured, str):
+        return captured
+    if argument.annotation is None:
+        raise definition.error(argument, "every CKL parameter requires a type annotation")
+    return resolve(argument.annotation, definition)
+
+
+# ------------------------------------------------------------------------- constants
+_INTEGER_BITS = {i32: 32, i64: 64, index: 64}
+
+
+def _round_f32(value: float) -> float:
+    return struct.unpack("<f", struct.pack("<f", value))[0]
+
+
+def _fits(value, dtype):
+    """`value` converted to `dtype`, or None when it does not fit."""
     if dtype == bool_:
-        if type(value) is bool:
-            return value
-    elif dtype in (i32, i64, index):
-        width = 32 if dtype == i32 else 64
-        if type(value) is int and -(1 << (width - 1)) <= value < (1 << (width - 1)):
-            return value
-    elif dtype in (f32, f64) and type(value) in (int, float):
+        return value if type(value) is bool else None
+    if dtype in _INTEGER_BITS:
+        half = 1 << (_INTEGER_BITS[dtype] - 1)
+        return value if type(value) is int and -half <= value < half else None
+    if dtype in (f32, f64) and type(value) in (int, float):
         try:
             converted = float(value)
             if dtype == f32:
-                converted = struct.unpack("f", struct.pack("f", converted))[0]
-            if math.isfinite(converted):
-                return converted
+                converted = _round_f32(converted)
         except (OverflowError, struct.error):
-            pass
-    shown = repr(value) if type(value) in (int, float, bool, str, type(None)) else f"<{type(value).__name__}>"
-    raise definition.error(node, f"constant {shown} does not fit {dtype.name}")
+            return None
+        return converted if math.isfinite(converted) else None
+    return None
 
 
+def constant(value, dtype: ScalarType, definition: Definition, node: ast.AST):
+    """A Python constant as a value of `dtype` (f32 values rounded to f32); diagnostic if it
+    does not fit."""
+    converted = _fits(value, dtype)
+    if converted is None:
+        shown = repr(value) if _is_plain(value) else f"<{type(value).__name__}>"
+        raise definition.error(node, f"constant {shown} does not fit {dtype.name}")
+    return converted
+
+
+def _is_plain(value) -> bool:
+    return value is None or type(value) in (int, float, bool, str)
+
+
+# ------------------------------------------------------------------------- signatures
 @dataclass(frozen=True)
 class BoundParameter:
+    """One parameter of a specialisation: runtime (dtype = BufferSpec or scalar type) or
+    constant (value set, is_constant True)."""
+
     name: str
     dtype: object
     value: object = None
@@ -81,65 +116,87 @@ class BoundParameter:
 @dataclass(frozen=True)
 class BoundSignature:
     parameters: tuple
-    dimensions: tuple
+    dimensions: tuple          # sorted (dimension name, size) pairs
 
     @property
     def runtime(self) -> tuple:
         return tuple(p for p in self.parameters if not p.is_constant)
 
 
-def annotation_of(definition: Definition, argument: ast.arg) -> object:
-    annotation = definition.annotations.get(argument.arg)
-    if annotation is None or isinstance(annotation, str):
-        if argument.annotation is None:
-            raise definition.error(argument, "every CKL parameter requires a type annotation")
-        annotation = resolve(argument.annotation, definition)
-    return annotation
+class _Binder:
+    def __init__(self, definition: Definition, signature: Mapping, constants: Mapping):
+        self.definition, self.signature, self.constants = definition, signature, constants
+        self.sizes = {}
+
+    def fail(self, node, message):
+        raise self.definition.error(node, message)
+
+    def check_parameter_list(self):
+        args = self.definition.tree.args
+        if args.posonlyargs or args.vararg or args.kwarg or args.kwonlyargs or args.defaults or args.kw_defaults:
+            self.fail(self.definition.tree, "CKL definitions require named positional parameters without defaults")
+        unknown = (set(self.signature) | set(self.constants)) - {a.arg for a in args.args}
+        if unknown:
+            self.fail(self.definition.tree, f"unknown specialization arguments: {sorted(unknown)}")
+        return args.args
+
+    def constexpr(self, argument, annotation: ConstexprType) -> BoundParameter:
+        name = argument.arg
+        if name not in self.constants or name in self.signature:
+            self.fail(argument, "constexpr parameters require a constants binding, not a runtime signature")
+        value = constant(self.constants[name], annotation.dtype, self.definition, argument)
+        return BoundParameter(name, annotation.dtype, value, True)
+
+    def unify(self, argument, expected: BufferType, actual: BufferSpec):
+        for declared, size in zip(expected.shape, actual.shape):
+            if isinstance(declared, Dimension):
+                known = self.sizes.setdefault(declared.name, size)
+                if known != size:
+                    self.fail(argument, f"dimension {declared.name} conflicts: {known} versus {size}")
+            elif declared != size:
+                self.fail(argument, f"fixed extent {declared} does not match {size}")
+
+    def runtime(self, argument, annotation) -> BoundParameter:
+        name = argument.arg
+        if name not in self.signature or name in self.constants:
+            self.fail(argument, f"missing or misplaced runtime signature for '{name}'")
+        actual = self.signature[name]
+        if isinstance(annotation, BufferType):
+            if not (isinstance(actual, BufferSpec) and actual.dtype == annotation.dtype
+                    and len(actual.shape) == len(annotation.shape)):
+                self.fail(argument, f"buffer type/rank mismatch for '{name}'")
+            self.unify(argument, annotation, actual)
+        elif any(annotation == t for t in NUMERIC_TYPES):
+            if not (isinstance(actual, ScalarType) and actual == annotation):
+                self.fail(argument, f"scalar type mismatch for '{name}'")
+        else:
+            self.fail(argument, "runtime parameters require numeric scalars or typed buffers")
+        return BoundParameter(name, actual)
+
+    def check_return(self):
+        tree = self.definition.tree
+        if tree.returns is None:
+            return
+        declared = self.definition.annotations.get("return")
+        if isinstance(declared, str):
+            declared = resolve(tree.returns, self.definition)
+        if declared is not None:
+            self.fail(tree.returns, "CKL entry points have no return values")
+
+    def bind(self) -> BoundSignature:
+        bound = []
+        for argument in self.check_parameter_list():
+            annotation = annotation_of(self.definition, argument)
+            if isinstance(annotation, ConstexprType):
+                bound.append(self.constexpr(argument, annotation))
+            else:
+                bound.append(self.runtime(argument, annotation))
+        self.check_return()
+        return BoundSignature(tuple(bound), tuple(sorted(self.sizes.items())))
 
 
 def bind(definition: Definition, signature: Mapping, constants: Mapping) -> BoundSignature:
+    """Specialise `definition` for `signature` and `constants`."""
     if not isinstance(signature, Mapping) or not isinstance(constants, Mapping):
         raise definition.error(definition.tree, "signature and constants must be mappings")
-    arguments = definition.tree.args
-    if arguments.posonlyargs or arguments.vararg or arguments.kwarg or arguments.kwonlyargs or \
-            arguments.defaults or arguments.kw_defaults:
-        raise definition.error(definition.tree, "CKL definitions require named positional parameters without defaults")
-    extra = (set(signature) | set(constants)) - {a.arg for a in arguments.args}
-    if extra:
-        raise definition.error(definition.tree, f"unknown specialization arguments: {sorted(extra)}")
-    result, dimensions = [], {}
-    for argument in arguments.args:
-        annotation = annotation_of(definition, argument)
-        if isinstance(annotation, ConstexprType):
-            if argument.arg not in constants or argument.arg in signature:
-                raise definition.error(argument, "constexpr parameters require a constants binding, not a runtime signature")
-            result.append(BoundParameter(argument.arg, annotation.dtype,
-                                         constant(constants[argument.arg], annotation.dtype, definition, argument), True))
-            continue
-        if argument.arg not in signature or argument.arg in constants:
-            raise definition.error(argument, f"missing or misplaced runtime signature for '{argument.arg}'")
-        actual = signature[argument.arg]
-        if isinstance(annotation, BufferType):
-            if not isinstance(actual, BufferSpec) or actual.dtype != annotation.dtype or \
-                    len(actual.shape) != len(annotation.shape):
-                raise definition.error(argument, f"buffer type/rank mismatch for '{argument.arg}'")
-            for expected, extent in zip(annotation.shape, actual.shape):
-                if isinstance(expected, Dimension):
-                    previous = dimensions.setdefault(expected.name, extent)
-                    if previous != extent:
-                        raise definition.error(argument, f"dimension {expected.name} conflicts: {previous} versus {extent}")
-                elif expected != extent:
-                    raise definition.error(argument, f"fixed extent {expected} does not match {extent}")
-        elif annotation in NUMERIC_TYPES:
-            if not isinstance(actual, ScalarType) or actual != annotation:
-                raise definition.error(argument, f"scalar type mismatch for '{argument.arg}'")
-        else:
-            raise definition.error(argument, "runtime parameters require numeric scalars or typed buffers")
-        result.append(BoundParameter(argument.arg, actual))
-    if definition.tree.returns is not None:
-        returned = definition.annotations.get("return")
-        if isinstance(returned, str):
-            returned = resolve(definition.tree.returns, definition)
-        if returned is not None:
-            raise definition.error(definition.tree.returns, "CKL entry points have no return values")
-    return BoundSignature(tuple(result), tuple(sorted(dimensions.items())))
+    return _Binder(definition, signature, constants).bind()
