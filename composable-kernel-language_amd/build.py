@@ -25,6 +25,9 @@ HOST_SOURCES = [
     "runtime/runtime.cpp", "runtime/chains.cpp", "runtime/codegen.cpp", "runtime/kernarg.cpp", "capi.cpp",
 ]
 KERNEL_SOURCES = ["kernels/library.hip"]
+# Host sources with device code of their own (the static scratch arena), built by hipcc into
+# objects of libckl_hip.so.
+HIP_HOST_SOURCES = ["runtime/scratch.hip"]
 # Packed FP32 instructions are disabled for all device code built here.
 DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
@@ -47,12 +50,24 @@ def compile_host(source: str) -> Path:
     return obj
 
 
+def compile_hip_host(source: str) -> Path:
+    obj = BUILD / (source.replace("/", "_") + ".o")
+    src = CSRC / source
+    deps = [src, *CSRC.glob("**/*.h"), ROOT.parent / "include" / "ckl_hip.h"]
+    if obj.exists() and obj.stat().st_mtime >= max(p.stat().st_mtime for p in deps):
+        return obj
+    run([str(ROCM / "bin" / "hipcc"), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", *DEVICE_FLAGS,
+         "-c", str(src), "-o", str(obj)])
+    return obj
+
+
 def build(jobs: int = 8) -> None:
     BUILD.mkdir(exist_ok=True)
     OUT.mkdir(parents=True, exist_ok=True)
     with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as pool:
         kernels = pool.submit(build_kernels)
-        objects = list(pool.map(compile_host, HOST_SOURCES))
+        hip_objects = [pool.submit(compile_hip_host, s) for s in HIP_HOST_SOURCES]
+        objects = list(pool.map(compile_host, HOST_SOURCES)) + [f.result() for f in hip_objects]
         kernels.result()
     library = OUT / "libckl_hip.so"
     tmp = library.with_suffix(".so.tmp")

@@ -335,6 +335,30 @@ int ckl_bind(ckl_program *program, ckl_device *device, const ckl_argument *argum
   });
 }
 
+int ckl_bind_static(ckl_program *program, ckl_device *device, const ckl_argument *arguments, size_t count,
+                    void *stream, ckl_invocation **out) {
+  return guarded([&] {
+    require(program, "program");
+    require(device, "device");
+    require(out, "out");
+    if (count && !arguments) throw std::invalid_argument("arguments must not be null");
+    std::vector<ckl::rt::Argument> args(count);
+    for (size_t k = 0; k < count; ++k) {
+      args[k].kind = arguments[k].kind;
+      if (arguments[k].kind == CKL_ARG_BUFFER) {
+        if (!arguments[k].buffer) throw std::invalid_argument("buffer argument must not be null");
+        args[k].buffer = arguments[k].buffer->buffer;
+      }
+      args[k].integer = arguments[k].integer;
+      args[k].real = arguments[k].real;
+    }
+    *out = new ckl_invocation{
+        ckl::rt::bindStatic(program->state, device->device, args, static_cast<hipStream_t>(stream))};
+  });
+}
+
+uint64_t ckl_static_scratch_bytes(void) { return CKL_STATIC_SCRATCH_BYTES; }
+
 int ckl_invocation_run(ckl_invocation *invocation, int mode, uint64_t batch) {
   return guarded([&] {
     require(invocation, "invocation");

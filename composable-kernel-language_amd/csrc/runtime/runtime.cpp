@@ -1,4 +1,5 @@
 #include "runtime.h"
+#include "scratch.h"
 
 #include <algorithm>
 #include <chrono>
@@ -42,10 +43,13 @@ Device::~Device() {
 
 void Device::makeCurrent() const { check(hipSetDevice(ordinal), "hipSetDevice"); }
 
-hipModule_t Device::load(const std::string &identity, const void *image, size_t bytes) {
+hipModule_t Device::load(const std::string &identity, const void *image, size_t bytes, bool allowLoad) {
   std::lock_guard<std::mutex> lock(moduleMutex);
   auto found = modules.find(identity);
   if (found != modules.end()) return found->second;
+  if (!allowLoad)
+    throw std::invalid_argument("code object " + identity + " is not resident on this device; a no-allocation bind "
+                                "cannot load it (bind the program once with ckl_bind first)");
   if (!image || !bytes) throw std::invalid_argument("cannot load an empty code object");
   std::map<std::string, KernelSignature> layouts = readKernelSignatures(image, bytes);
   makeCurrent();
@@ -451,10 +455,15 @@ std::unique_ptr<GraphExec> explicitGraph(const Plan &plan, const std::vector<Uni
 } // namespace
 
 // ====================================================================== invocation
-Invocation::Invocation(std::shared_ptr<ProgramState> program_, std::shared_ptr<Device> device_)
+Invocation::Invocation(std::shared_ptr<ProgramState> program_, std::shared_ptr<Device> device_, hipStream_t external)
     : program(std::move(program_)), device(std::move(device_)) {
   device->makeCurrent();
-  check(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "hipStreamCreateWithFlags");
+  if (external) {
+    stream = external;
+    ownsStream = false;
+  } else {
+    check(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "hipStreamCreateWithFlags");
+  }
 }
 
 Invocation::~Invocation() {
@@ -462,11 +471,30 @@ Invocation::~Invocation() {
   if (stream) {
     device->makeCurrent();
     hipStreamSynchronize(stream);
-    hipStreamDestroy(stream);
+    if (ownsStream) hipStreamDestroy(stream);
   }
 }
 
+uint64_t Invocation::carve(uint64_t bytes) {
+  const uint64_t start = (arenaUsed + 255) & ~uint64_t(255);
+  if (!bytes || start > arenaLimit || bytes > arenaLimit - start) {
+    arenaExceeded = true;
+    throw std::invalid_argument("the program needs more than the static arena's " + std::to_string(arenaLimit) +
+                                " bytes (CKL_STATIC_SCRATCH_BYTES) of heaps and workspaces");
+  }
+  arenaUsed = start + bytes;
+  return arenaBase + start;
+}
+
+namespace {
+constexpr int kMaxStaticDevices = 64;
+std::array<std::atomic<uint64_t>, kMaxStaticDevices> staticEpochs{};
+} // namespace
+
 void Invocation::validate(int mode, uint64_t batch) const {
+  if (staticArena && staticEpochs[size_t(device->ordinal)].load() != epoch)
+    throw std::invalid_argument("this invocation's static arena was taken over by a later ckl_bind_static on the same "
+                                "device; bind it again");
   if (mode < kOrdinary || mode > kContractedCapture || !batch || plan.nodes.empty() ||
       batch > 1000000 / plan.nodes.size())
     throw std::invalid_argument("invalid execution mode or batch exceeds one million kernel nodes");
@@ -689,8 +717,25 @@ static void appendArgument(Launch &launch, const void *data, uint64_t size, int6
   launch.slotResources.push_back(resource);
 }
 
-std::shared_ptr<Invocation> bind(const std::shared_ptr<ProgramState> &programIn, std::shared_ptr<Device> device,
+static std::shared_ptr<Invocation> bindWith(const std::shared_ptr<ProgramState> &programIn, std::shared_ptr<Device> device,
+                                            const std::vector<Argument> &arguments, bool arena, hipStream_t stream);
+
+std::shared_ptr<Invocation> bind(const std::shared_ptr<ProgramState> &program, std::shared_ptr<Device> device,
                                  const std::vector<Argument> &arguments) {
+  return bindWith(program, std::move(device), arguments, false, nullptr);
+}
+
+std::shared_ptr<Invocation> bindStatic(const std::shared_ptr<ProgramState> &program, std::shared_ptr<Device> device,
+                                       const std::vector<Argument> &arguments, hipStream_t stream) {
+  if (!device) throw std::invalid_argument("program binding requires a device");
+  if (!stream) throw std::invalid_argument("a no-allocation bind needs the caller's stream");
+  if (device->ordinal < 0 || device->ordinal >= kMaxStaticDevices)
+    throw std::invalid_argument("HIP device ordinal out of range for the static arena");
+  return bindWith(program, std::move(device), arguments, true, stream);
+}
+
+static std::shared_ptr<Invocation> bindWith(const std::shared_ptr<ProgramState> &programIn, std::shared_ptr<Device> device,
+                                            const std::vector<Argument> &arguments, bool arena, hipStream_t stream) {
   auto program = programIn;
   if (!device) throw std::invalid_argument("program binding requires a device");
   size_t count = arguments.size();
@@ -729,13 +774,25 @@ std::shared_ptr<Invocation> bind(const std::shared_ptr<ProgramState> &programIn,
       }
     if (overlap) program = program->aliasFallback;
   }
-  auto invocation = std::make_shared<Invocation>(program, device);
+  auto invocation = std::make_shared<Invocation>(program, device, stream);
   invocation->buffers = std::move(buffers);
+  if (arena) {
+    invocation->staticArena = true;
+    invocation->arenaBase = staticScratchAddress(device->ordinal);
+    invocation->arenaLimit = staticScratchBytes();
+    // Every static bind on a device reuses the arena from its start: earlier ones are superseded.
+    invocation->epoch = ++staticEpochs[size_t(device->ordinal)];
+  }
   void *frame = invocation.get();
   void **values = packed.data();
   void *entryArguments[] = {&frame, &values, program->entryContext};
   program->entry(entryArguments);
-  if (!invocation->error.empty()) throw std::runtime_error(invocation->error);
+  if (!invocation->error.empty()) {
+    // The reference reports callback failures as runtime errors; a program too large for the
+    // static arena is the caller's argument error.
+    if (invocation->arenaExceeded) throw std::invalid_argument(invocation->error);
+    throw std::runtime_error(invocation->error);
+  }
   return invocation;
 }
 
@@ -751,14 +808,15 @@ extern "C" void ckl_begin(void *frame, const void *binary, uint64_t bytes) {
 extern "C" void ckl_module(void *frame, const char *identity, const void *binary, uint64_t bytes) {
   ckl::rt::callback(frame, [&](Invocation &f) {
     std::string key = identity && *identity ? identity : "program:" + std::to_string(reinterpret_cast<uintptr_t>(f.program.get()));
-    f.module = f.device->load(key, binary, bytes);
+    f.module = f.device->load(key, binary, bytes, !f.staticArena);
   });
 }
 
 extern "C" void ckl_heap(void *frame, uint64_t id, uint64_t bytes) {
   ckl::rt::callback(frame, [&](Invocation &f) {
     if (f.heaps.size() <= id) f.heaps.resize(id + 1);
-    f.heaps[id] = ckl::rt::allocateBuffer(f.device, bytes);
+    f.heaps[id] = f.staticArena ? ckl::rt::importBuffer(f.device, f.carve(bytes), bytes)
+                                : ckl::rt::allocateBuffer(f.device, bytes);
   });
 }
 
@@ -810,10 +868,18 @@ extern "C" void ckl_argument_value(void *frame, const void *bytes, uint64_t size
 extern "C" void ckl_workspace(void *frame, uint64_t bytes) {
   ckl::rt::callback(frame, [&](Invocation &f) {
     if (!bytes) throw std::invalid_argument("library workspace must be non-empty");
-    auto buffer = ckl::rt::allocateBuffer(f.device, bytes);
+    std::shared_ptr<ckl::rt::Buffer> buffer;
     f.device->makeCurrent();
-    ckl::rt::check(hipMemset(reinterpret_cast<void *>(buffer->address()), 0, bytes), "hipMemset(workspace)");
-    ckl::rt::check(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    if (f.staticArena) {
+      // The arena keeps whatever the last user left: clear the workspace on the caller's stream.
+      const uint64_t rounded = (bytes + 15) & ~uint64_t(15);
+      buffer = ckl::rt::importBuffer(f.device, f.carve(rounded), rounded);
+      ckl::rt::staticScratchClear(buffer->address(), rounded, f.stream);
+    } else {
+      buffer = ckl::rt::allocateBuffer(f.device, bytes);
+      ckl::rt::check(hipMemset(reinterpret_cast<void *>(buffer->address()), 0, bytes), "hipMemset(workspace)");
+      ckl::rt::check(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    }
     uint64_t address = buffer->address();
     ckl::rt::appendArgument(f.pending, &address, sizeof address);
     f.workspaces.push_back(std::move(buffer));

@@ -41,7 +41,9 @@ struct Device {
   std::map<std::string, hipModule_t> modules;   // artifact identity -> loaded module
   // Explicit argument layout of every kernel of every loaded module (from its metadata note).
   std::map<hipFunction_t, KernelSignature> signatures;
-  hipModule_t load(const std::string &identity, const void *image, size_t bytes);
+  // Loads (once) the code object `identity`; with `allowLoad` false a module that is not yet
+  // resident is an error instead (the no-allocation bind may not load code objects).
+  hipModule_t load(const std::string &identity, const void *image, size_t bytes, bool allowLoad = true);
   // Layout of a kernel of a module loaded here; throws std::logic_error for an unknown function.
   const KernelSignature &signature(hipFunction_t function);
   void makeCurrent() const;
@@ -154,7 +156,16 @@ struct Invocation {
   std::mutex runMutex;
   std::string error;
 
-  Invocation(std::shared_ptr<ProgramState> program, std::shared_ptr<Device> device);
+  // No-allocation binding (ckl_bind_static): heaps and workspaces are carved from the device's
+  // static arena at [arenaBase, arenaBase + arenaLimit); `epoch` is the device's static-bind
+  // count when this invocation was bound (a later static bind on the device supersedes it).
+  bool staticArena = false;
+  uint64_t arenaBase = 0, arenaUsed = 0, arenaLimit = 0, epoch = 0;
+  bool ownsStream = true;
+  bool arenaExceeded = false;                       // the static arena was too small (bind fails)
+  uint64_t carve(uint64_t bytes);                   // 256-aligned arena range for `bytes`
+
+  Invocation(std::shared_ptr<ProgramState> program, std::shared_ptr<Device> device, hipStream_t external = nullptr);
   ~Invocation();
   void run(int mode, uint64_t batch);
   std::array<double, 3> benchmark(int mode, uint64_t iterations, uint64_t batch);
@@ -207,6 +218,11 @@ struct Argument {
 
 std::shared_ptr<Invocation> bind(const std::shared_ptr<ProgramState> &program, std::shared_ptr<Device> device,
                                  const std::vector<Argument> &arguments);
+// bind without any device allocation: heaps and library workspaces in the device's static arena
+// (workspaces cleared by a kernel on `stream`), launches on the caller's `stream`, code objects
+// already resident on the device. Supersedes every earlier static binding on that device.
+std::shared_ptr<Invocation> bindStatic(const std::shared_ptr<ProgramState> &program, std::shared_ptr<Device> device,
+                                       const std::vector<Argument> &arguments, hipStream_t stream);
 
 // CKL_INFERRED_STREAM=1: modes 1 and 4 issue the contracted launch chain as ordinary stream
 // launches instead of one graph launch (same kernels and order; for per-kernel profiling).

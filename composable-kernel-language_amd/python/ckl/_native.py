@@ -69,6 +69,9 @@ _SIGNATURES = {
     "ckl_buffer_release": ([ctypes.c_void_p], None),
     "ckl_bind": ([ctypes.c_void_p, ctypes.c_void_p, ctypes.POINTER(Argument), ctypes.c_size_t, ctypes.POINTER(ctypes.c_void_p)],
                  ctypes.c_int),
+    "ckl_bind_static": ([ctypes.c_void_p, ctypes.c_void_p, ctypes.POINTER(Argument), ctypes.c_size_t, ctypes.c_void_p,
+                         ctypes.POINTER(ctypes.c_void_p)], ctypes.c_int),
+    "ckl_static_scratch_bytes": ([], ctypes.c_uint64),
     "ckl_invocation_run": ([ctypes.c_void_p, ctypes.c_int, ctypes.c_uint64], ctypes.c_int),
     "ckl_invocation_benchmark": ([ctypes.c_void_p, ctypes.c_int, ctypes.c_uint64, ctypes.c_uint64,
                                   ctypes.POINTER(ctypes.c_double)], ctypes.c_int),

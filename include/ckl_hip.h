@@ -138,6 +138,25 @@ typedef struct {
  * invocation (one stream, one allocation per planned heap). */
 int ckl_bind(ckl_program *program, ckl_device *device, const ckl_argument *arguments, size_t count,
              ckl_invocation **out);
+/* No-allocation variant of ckl_bind. No counterpart in the reference: it is for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc). It calls no hipMalloc/hipFree or other allocating routine:
+ *  - planned heaps and library workspaces are carved from a static arena of
+ *    CKL_STATIC_SCRATCH_BYTES per device (a file-scope device array of the library, held until
+ *    the process ends); larger programs are refused with CKL_INVALID_ARGUMENT;
+ *  - workspaces are cleared by a kernel enqueued on `stream` (a caller-owned hipStream_t, which
+ *    the invocation launches on and never destroys);
+ *  - every code object of the program must already be resident on the device (bind it once
+ *    with ckl_bind); otherwise CKL_INVALID_ARGUMENT.
+ * All static bindings on one device share that arena from its start: a later ckl_bind_static on
+ * the device supersedes earlier ones (running a superseded invocation fails with
+ * CKL_INVALID_ARGUMENT), and work of two static invocations that overlaps on one device races. */
+#define CKL_STATIC_SCRATCH_BYTES (64ull << 20)
+int ckl_bind_static(ckl_program *program, ckl_device *device, const ckl_argument *arguments, size_t count,
+                    void *stream, ckl_invocation **out);
+/* CKL_STATIC_SCRATCH_BYTES, for bindings that cannot read the macro. */
+uint64_t ckl_static_scratch_bytes(void);
+
 /* mode: 0 ordinary launches, 1 inferred graph, 2 single-stream capture (the reference's three,
  * lib/Runtime/NvidiaProgram.cpp:115-131), plus two ablations of mode 1 with no reference
  * counterpart as separate modes: 3 one kernel node per dispatch with the reduced DAG's edges (the
