@@ -175,7 +175,7 @@ class _Binder:
 
     def check_return(self):
         tree = self.definition.tree
-        if tree.returns is None:
+        if tree.returns is None or self.definition.kind == "block":   # blocks may return buffers
             return
         declared = self.definition.annotations.get("return")
         if isinstance(declared, str):

@@ -391,18 +391,27 @@ class Lowering:
         target = node.targets[0]
         value = self.evaluate(node.value)
         if isinstance(target, ast.Name):
-            if value is None:
-                self.fail(node, "launches do not return source values")
-            if self.deferred is not None and target.id in self.deferred:
-                self.fail(target, "runtime branch results are deferred; write buffers or use branch-local variables")
-            previous = self.scope.get(target.id)
-            if _scalar(previous):
-                value = self.as_type(value, previous.dtype, node.value)
-            self.scope[target.id] = value
+            self.bind_name(target, value, node)
         elif isinstance(target, ast.Subscript):
             self.store(target, value, node)
+        elif isinstance(target, ast.Tuple) and all(isinstance(t, ast.Name) for t in target.elts):
+            # Destructuring of a compile-time tuple (a shape, or the buffers a block returns).
+            if type(value) is not tuple or len(value) != len(target.elts):
+                self.fail(target, "tuple assignment requires a tuple of the same length")
+            for name, item in zip(target.elts, value):
+                self.bind_name(name, item, node)
         else:
             self.fail(target, "assignment requires a local name or indexed buffer element")
+
+    def bind_name(self, target: ast.Name, value, node):
+        if value is None:
+            self.fail(node, "launches do not return source values")
+        if self.deferred is not None and target.id in self.deferred:
+            self.fail(target, "runtime branch results are deferred; write buffers or use branch-local variables")
+        previous = self.scope.get(target.id)
+        if _scalar(previous):
+            value = self.as_type(value, previous.dtype, node.value)
+        self.scope[target.id] = value
 
     def stmt_If(self, node, last, first, top):
         predicate = self.evaluate(node.test)

@@ -4,7 +4,8 @@
 parse it; the body is never executed. Every name the body or its annotations use is looked up
 once, in the function's globals and closure, and classified: compile-time constants (ints,
 floats, bools, strings, None and tuples of them), CKL types and dimensions, other definitions,
-intrinsics and the `ckl` module itself are kept; anything else is recorded as unsupported and
+intrinsics, the `ckl` module and modules of CKL definitions are kept; anything else is recorded
+as unsupported and
 reported only if the body actually evaluates it. A definition's identity is a SHA-256 over its
 syntax tree and those captured values, so edits to a kernel or to a constant it reads change it.
 
@@ -62,7 +63,7 @@ RANGE = Intrinsic("range")
 
 
 class Namespace:
-    """The `ckl` module as a definition sees it: its scalar types, intrinsics and annotation syntax."""
+    """A module as a definition sees it (`ckl`, or a module of kernels): its CKL members."""
 
     def __init__(self, values):
         self.values = MappingProxyType(dict(values))
@@ -88,9 +89,16 @@ def _is_ckl_value(value) -> bool:
 
 
 def _module_namespace(module: ModuleType) -> Namespace:
+    """The `ckl` module exposes its scalar types, intrinsics and annotation syntax; any other
+    module exposes the CKL values and constants it defines (kernels, blocks, dimensions, types),
+    so `module.kernel_name` works in launches."""
     exported = {}
     for key, item in vars(module).items():
+        if key.startswith("__"):
+            continue
         if isinstance(item, (ScalarType, Intrinsic)) or item is Buffer or item is constexpr:
+            exported[key] = item
+        elif module.__name__ != "ckl" and (_is_ckl_value(item) or _is_constant(item)):
             exported[key] = item
     return Namespace(exported)
 
@@ -101,7 +109,7 @@ def classify(name: str, value):
         return RANGE
     if _is_constant(value) or _is_ckl_value(value):
         return value
-    if isinstance(value, ModuleType) and value.__name__ == "ckl":
+    if isinstance(value, ModuleType):
         return _module_namespace(value)
     return UnsupportedBinding(name)
 

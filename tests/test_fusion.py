@@ -36,14 +36,15 @@ def test_two_stage_chain_is_scalarised_deterministically():
     assert executable.count('"ckl_exec.kernel"') == 1 and '"ckl_exec.heap"' not in executable
 
 
-@pytest.mark.parametrize("name,expected", [("single_affine", 1), ("chain_six", 1), ("fork_join", 6), ("stencil_two", 2)])
-def test_complete_chains_fuse_but_not_branches_or_stencils(name, expected):
+@pytest.mark.parametrize("name", sorted(CASES))
+def test_complete_chains_fuse_but_not_branches_or_stencils(name):
+    program, expected = CASES[name]
     signature = {"src": SPEC, "dst": SPEC}
-    if name == "fork_join":
+    if name == "fan_out":
         signature["other"] = SPEC
-    out = fused(CASES[name].lower(signature=signature).mlir)
+    out = fused(program.lower(signature=signature).mlir)
     assert out.count('"ckl.dispatch"') == expected
-    if name == "chain_six":
+    if name == "six_steps":
         assert "ckl.fused_steps = 6" in out and '"ckl.alloc"' not in out
 
 

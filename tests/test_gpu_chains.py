@@ -6,7 +6,7 @@ import pytest
 
 import ckl
 from oracle import decoder as oracle
-from programs.decoder import rms_apply, rms_stats
+from ckl.decoder_kernels import rms_apply, rms_stats
 from ckl.library import linear_tiling
 from programs.decoder_config import CONFIGS, Config
 from programs.harness import MUTABLE, DecoderSession

@@ -6,7 +6,7 @@ import numpy as np
 import pytest
 
 import ckl
-from fusion_programs import rounding
+from fusion_programs import scale_offset
 from programs import vector_pipeline
 
 pytestmark = pytest.mark.gpu
@@ -72,7 +72,7 @@ def test_fusion_keeps_f32_rounding_of_the_removed_store(device):
     """(1 + 2^-23)(1 - 2^-23) rounds to 1 in f32, so the fused multiply-then-shift by -1 gives
     exactly 0; a contracted fma would give -2^-46."""
     spec = ckl.BufferSpec((257,), ckl.f32)
-    program = rounding.lower(signature={"src": spec, "dst": spec, "factor": ckl.f32, "bias": ckl.f32}).compile()
+    program = scale_offset.lower(signature={"src": spec, "dst": spec, "factor": ckl.f32, "bias": ckl.f32}).compile()
     src, dst = device.empty(spec), device.empty(spec)
     src.copy_from_host(np.full(257, 1 + 2 ** -23, np.float32))
     invocation = program.bind(src, dst, 1 - 2 ** -23, -1.0)

@@ -10,8 +10,8 @@ import pytest
 
 import ckl
 from oracle import decoder as oracle
-from programs.decoder import History, Logits, Position, Tokens, advance, greedy, linear
-from programs.decoder import B as _B
+from ckl.decoder_kernels import _B, advance, greedy, linear
+from ckl.decoder_kernels import _History as History, _Logits as Logits, _Position as Position, _Tokens as Tokens
 from test_oracle_decoder import edge_rows
 
 pytestmark = pytest.mark.gpu

@@ -12,7 +12,7 @@ import pytest
 
 import ckl
 from ckl.library import linear_tiling
-from programs.decoder import linear
+from ckl.decoder_kernels import linear
 
 pytestmark = pytest.mark.gpu
 

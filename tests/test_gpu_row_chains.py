@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 import ckl
-from programs.decoder import add, embedding, linear, rms_apply, rms_stats
+from ckl.decoder_kernels import add, embedding, linear, rms_apply, rms_stats
 
 pytestmark = pytest.mark.gpu
 
