@@ -667,84 +667,9 @@ __device__ __forceinline__ void mfma_compute(const MfmaStage<J, S, M> &st, float
           acc[m][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(st.x[u][i], st.w[m][u][i][j], acc[m][j], 0, 0, 0);
 }
 
-// Split-bf16 flavour: v_mfma_f32_32x32x16_bf16 at 16x the f32 MFMA rate. Every f32 operand is split
-// exactly into three bf16 parts, v = hi + mid + lo (hi = RNE(v), mid = RNE(v - hi), lo = RNE of the
-// rest), and each 16-row K-step accumulates the six products whose magnitude is above 2^-24 of
-// x*w: hi*hi, hi*mid, mid*hi, hi*lo, lo*hi, mid*mid. The dropped terms are below 2^-23 |x*w|,
-// the size of an f32 rounding, and products of bf16 parts are exact in the f32 accumulator. A
-// lane's 8 K values are rows {k + 8u + 4s + i} of the same permuted K order as the f32 flavour
-// (A and B permuted alike leave the dot product unchanged). An infinite hi part (an infinite
-// operand, or one beyond the bf16 range) keeps mid = lo = 0, so infinities propagate as in f32.
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-struct SplitBf16 { unsigned hi[4], mid[4], lo[4]; };
-
-__device__ __forceinline__ unsigned pack_bf16(float a, float b) {
-  bf16x2 v = {(__bf16)a, (__bf16)b};       // v_cvt_pk_bf16_f32: round to nearest even
-  return __builtin_bit_cast(unsigned, v);
-}
-__device__ __forceinline__ float bf16_low(unsigned p) { return __uint_as_float(p << 16); }
-__device__ __forceinline__ float bf16_high(unsigned p) { return __uint_as_float(p & 0xFFFF0000u); }
-
-__device__ __forceinline__ void split_bf16(const float (&v)[8], SplitBf16 &out) {
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const float a = v[2 * e], b = v[2 * e + 1];
-    const unsigned h = pack_bf16(a, b);
-    const float ha = bf16_low(h), hb = bf16_high(h);
-    const float ra = __builtin_isinf(ha) ? 0.f : a - ha, rb = __builtin_isinf(hb) ? 0.f : b - hb;
-    const unsigned m = pack_bf16(ra, rb);
-    out.hi[e] = h;
-    out.mid[e] = m;
-    out.lo[e] = pack_bf16(ra - bf16_low(m), rb - bf16_high(m));
-  }
-}
-
-__device__ __forceinline__ bf16x8 as_bf16x8(const unsigned (&p)[4]) {
-  return __builtin_bit_cast(bf16x8, make_uint4(p[0], p[1], p[2], p[3]));
-}
-
-template <int J, int S, int M>
-__device__ __forceinline__ void mfma_compute_bf16(const MfmaStage<J, S, M> &st, floatx16 (&acc)[M][J]) {
-#pragma unroll
-  for (int t = 0; t < S; ++t) {
-    float xv[8];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) { xv[i] = st.x[2 * t][i]; xv[4 + i] = st.x[2 * t + 1][i]; }
-    SplitBf16 xs;
-    split_bf16(xv, xs);
-    const bf16x8 xh = as_bf16x8(xs.hi), xm = as_bf16x8(xs.mid), xl = as_bf16x8(xs.lo);
-#pragma unroll
-    for (int m = 0; m < M; ++m)
-#pragma unroll
-      for (int j = 0; j < J; ++j) {
-        float wv[8];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) { wv[i] = st.w[m][2 * t][i][j]; wv[4 + i] = st.w[m][2 * t + 1][i][j]; }
-        SplitBf16 ws;
-        split_bf16(wv, ws);
-        const bf16x8 wh = as_bf16x8(ws.hi), wm = as_bf16x8(ws.mid), wl = as_bf16x8(ws.lo);
-        floatx16 &c = acc[m][j];
-        c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xm, wm, c, 0, 0, 0);
-        c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xl, wh, c, 0, 0, 0);
-        c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh, wl, c, 0, 0, 0);
-        c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xm, wh, c, 0, 0, 0);
-        c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh, wm, c, 0, 0, 0);
-        c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(xh, wh, c, 0, 0, 0);
-      }
-  }
-}
-
-enum class MfmaFlavour { F32, SplitBf16 };
-template <MfmaFlavour F, int J, int S, int M>
-__device__ __forceinline__ void stage_compute(const MfmaStage<J, S, M> &st, floatx16 (&acc)[M][J]) {
-  if constexpr (F == MfmaFlavour::F32) mfma_compute<J, S, M>(st, acc);
-  else mfma_compute_bf16<J, S, M>(st, acc);
-}
-
 // `a` holds M member blocks that agree on x, B, I, O, layer and the tiling (M = 1: one linear);
 // the workgroup computes its tile of every member from one stream of x fragments.
-template <MfmaFlavour F, int J, int S, int M, bool NT>
+template <int J, int S, int M, bool NT>
 __device__ void linear_mfma(const LinearArgs *a, int block, float *smem) {
   const LinearArgs &a0 = a[0];
   const int lane = threadIdx.x & 63;
@@ -790,22 +715,22 @@ __device__ void linear_mfma(const LinearArgs *a, int block, float *smem) {
   for (; t + 1 < full; t += 2) {
     mfma_load<J, S, M, false, NT>(sb, xr, w, O, k + 4 * R * (t + 1), k1);
     __builtin_amdgcn_sched_barrier(0);
-    stage_compute<F, J, S, M>(sa, acc);
+    mfma_compute<J, S, M>(sa, acc);
     __builtin_amdgcn_sched_barrier(0);
     mfma_load<J, S, M, false, NT>(sa, xr, w, O, k + 4 * R * min(t + 2, full - 1), k1, t + 2 >= full,
                                   reinterpret_cast<const float *>(a0.workspace));
     __builtin_amdgcn_sched_barrier(0);
-    stage_compute<F, J, S, M>(sb, acc);
+    mfma_compute<J, S, M>(sb, acc);
     __builtin_amdgcn_sched_barrier(0);
   }
-  if (t < full) stage_compute<F, J, S, M>(sa, acc);
+  if (t < full) mfma_compute<J, S, M>(sa, acc);
   const int tailBase = kb0 + R * fullTotal;
   const int tailStages = (kb1 - tailBase + 15) / 16;
 #pragma unroll 1
   for (int q = (wave - fullTotal % 4 + 4) % 4; q < tailStages; q += 4) {
     MfmaStage<J, 1, M> st;
     mfma_load<J, 1, M, true, NT>(st, xr, w, O, tailBase + 16 * q + 4 * s, k1);
-    stage_compute<F, J, 1, M>(st, acc);
+    mfma_compute<J, 1, M>(st, acc);
   }
 
   // Every wave hands its tile to the others through LDS; wave w then adds rows {8w + 4s + q} of
@@ -943,11 +868,7 @@ template <bool NT> __device__ void linear_rowvec_stream(const LinearArgs &a, int
 
 template <int J, int S, bool NT = false> __device__ void linear_mfma_body(const LinearArgs &a, int block) {
   extern __shared__ float smem[];
-  linear_mfma<MfmaFlavour::F32, J, S, 1, NT>(&a, block, smem);
-}
-template <int J, int S> __device__ void linear_split_body(const LinearArgs &a, int block) {
-  extern __shared__ float smem[];
-  linear_mfma<MfmaFlavour::SplitBf16, J, S, 1, false>(&a, block, smem);
+  linear_mfma<J, S, 1, NT>(&a, block, smem);
 }
 CKL_ENTRY_ATTR(linear_rowvec, LinearArgs, linear_rowvec_stream<false>, 1024, )
 CKL_ENTRY_ATTR(linear_rowvec_nt, LinearArgs, linear_rowvec_stream<true>, 1024, )
@@ -963,13 +884,6 @@ CKL_ENTRY_ATTR(linear_mfma2x4, LinearArgs, (linear_mfma_body<2, 4>), kBlock, CKL
 CKL_ENTRY_ATTR(linear_mfma4x1, LinearArgs, (linear_mfma_body<4, 1>), kBlock, CKL_TWO_WAVES)
 CKL_ENTRY_ATTR(linear_mfma4x1_nt, LinearArgs, (linear_mfma_body<4, 1, true>), kBlock, CKL_TWO_WAVES)
 CKL_ENTRY_ATTR(linear_mfma4x2, LinearArgs, (linear_mfma_body<4, 2>), kBlock, CKL_TWO_WAVES)
-// ckl_linear_split<J>x<S>: the same tiling with the split-bf16 MFMA flavour.
-CKL_ENTRY(linear_split1x1, LinearArgs, (linear_split_body<1, 1>))
-CKL_ENTRY(linear_split1x2, LinearArgs, (linear_split_body<1, 2>))
-CKL_ENTRY_ATTR(linear_split2x1, LinearArgs, (linear_split_body<2, 1>), kBlock, CKL_TWO_WAVES)
-CKL_ENTRY_ATTR(linear_split2x2, LinearArgs, (linear_split_body<2, 2>), kBlock, CKL_TWO_WAVES)
-CKL_ENTRY_ATTR(linear_split4x1, LinearArgs, (linear_split_body<4, 1>), kBlock, CKL_TWO_WAVES)
-CKL_ENTRY_ATTR(linear_split4x2, LinearArgs, (linear_split_body<4, 2>), kBlock, CKL_TWO_WAVES)
 // ckl_linear_mfma<J>x1_shared<M>: M linears of one shape and tiling that multiply the same x
 // (their blocks in a Group<LinearArgs>, count == M; grid = one member's grid). Each workgroup
 // computes its tile of every member from one x stream, so the sibling projections of a decoder
@@ -978,12 +892,12 @@ CKL_ENTRY_ATTR(linear_split4x2, LinearArgs, (linear_split_body<4, 2>), kBlock, C
   extern "C" __global__ __launch_bounds__(kBlock) CKL_ONE_WAVE void ckl_linear_mfma##J##x1_shared##M( \
       const Group<LinearArgs> g) {                                                                    \
     extern __shared__ float smem[];                                                                   \
-    linear_mfma<MfmaFlavour::F32, J, 1, M, false>(g.m, blockIdx.x, smem);                             \
+    linear_mfma<J, 1, M, false>(g.m, blockIdx.x, smem);                             \
   }                                                                                                   \
   extern "C" __global__ __launch_bounds__(kBlock) CKL_ONE_WAVE void ckl_linear_mfma##J##x1_nt_shared##M( \
       const Group<LinearArgs> g) {                                                                    \
     extern __shared__ float smem[];                                                                   \
-    linear_mfma<MfmaFlavour::F32, J, 1, M, true>(g.m, blockIdx.x, smem);                              \
+    linear_mfma<J, 1, M, true>(g.m, blockIdx.x, smem);                              \
   }
 CKL_LINEAR_SHARED(1, 2)
 CKL_LINEAR_SHARED(1, 3)
