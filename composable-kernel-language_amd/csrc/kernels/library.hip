@@ -996,16 +996,18 @@ __device__ __forceinline__ float score_scalar(const float *q, const float *key, 
   return v;
 }
 // Vector layout of the scores: groups of G lanes hold one cache row, each lane P float4 pieces of
-// it (pieces part + G*j, j < P): P = 1 and G = D/4 for D <= 32, else G = 8 lanes (G = 16 for
-// D = 256) and P = D/32 (at most 4). Each lane adds its 4P products with explicit FMAs in piece
-// order, then the row is summed over its G lanes (group_sum), so with 8-lane groups a row costs
-// three DPP steps instead of a 32-lane butterfly. A wave load covers 64/G rows; a lane keeps
-// kScoreBatch pieces in flight (kScoreBatch/P rows).
+// it (pieces part + G*j, j < P): P = 1 and G = D/4 for D <= 32, P = 2 for D <= 64, else P = 4,
+// with G = D/(4P) a power of two (8 lanes for D = 64 and 128, 16 for D = 256); other D take the
+// sequential dot product. Each lane adds its 4P products with explicit FMAs in piece order, then
+// the row is summed over its G lanes (group_sum), so with 8-lane groups a row costs three DPP
+// steps instead of a 32-lane butterfly. A wave load covers 64/G rows; a lane keeps kScoreBatch
+// pieces in flight (kScoreBatch/P rows).
+__device__ __forceinline__ int score_pieces(int D) { return D <= 32 ? 1 : D <= 64 ? 2 : 4; }
 __device__ __forceinline__ bool scores_vector_layout(int D) {
   if ((D & 3) || D > 256) return false;
-  return D <= 32 ? (64 % (D / 4)) == 0 : (D % 32) == 0;
+  const int P = score_pieces(D), G = D / (4 * P);
+  return G * 4 * P == D && (G & (G - 1)) == 0;        // G lanes a row: a power of two
 }
-__device__ __forceinline__ int score_pieces(int D) { return D <= 32 ? 1 : min(D / 32, 4); }
 // Partial dot product of a lane's P pieces of q and of one key row.
 template <int P> __device__ __forceinline__ float dot_pieces(const float4 (&q)[P], const float4 *k) {
   float v = q[0].x * k[0].x;
@@ -1445,6 +1447,8 @@ __device__ void rope_attention_rows(const RopeAttentionChainArgs &a, int block) 
       *reinterpret_cast<float2 *>(ap.kc + row) = kr;
       *reinterpret_cast<float2 *>(ap.vc + row) = source2(a.v, ap.v, c);
     }
+    // The sequential dot product reads the appended key row from the cache after the barrier.
+    if (!vector) __builtin_amdgcn_s_waitcnt(kWaitStores);
   }
   __syncthreads();
   // The barrier alone does not wait for vector stores: the waves that appended cache rows wait for

@@ -21,6 +21,12 @@ ODD = Config(batch=2, hidden=42, heads=3, layers=2, ffn=31, vocab=70, context=5,
 # vector path (B <= 16, reductions over 1024 rows).
 SPLIT_MFMA = Config(batch=20, hidden=1024, heads=8, layers=1, ffn=1536, vocab=300, context=4, steps=3)
 SPLIT_VECTOR = Config(batch=5, hidden=1280, heads=10, layers=1, ffn=1536, vocab=300, context=4, steps=3)
+# Long cache rows for the other vector layouts of the attention (D = 64: 2 pieces a lane, D = 256:
+# 16 lanes a row), so that every wave's key and value streams wrap their rings several times;
+# and D = 96, whose rows take the sequential dot product and the scalar values loop.
+HEAD64 = Config(batch=2, hidden=128, heads=2, layers=1, ffn=96, vocab=100, context=300, steps=4)
+HEAD256 = Config(batch=2, hidden=512, heads=2, layers=1, ffn=64, vocab=100, context=150, steps=4)
+HEAD96 = Config(batch=2, hidden=192, heads=2, layers=1, ffn=64, vocab=100, context=40, steps=4)
 
 
 def whole_rows(b, i, o):
@@ -52,8 +58,10 @@ def chained_launches(c):
     return 1 + (2 + o + gate_up + down - merged) * c.layers + 2 - first - last
 
 
-@pytest.mark.parametrize("config", [CONFIGS["small"], REFERENCE_SMALL, AWKWARD, ODD, SPLIT_MFMA, SPLIT_VECTOR],
-                         ids=["small", "reference_small", "awkward", "odd", "split_mfma", "split_vector"])
+@pytest.mark.parametrize("config", [CONFIGS["small"], REFERENCE_SMALL, AWKWARD, ODD, SPLIT_MFMA, SPLIT_VECTOR, HEAD64,
+                                    HEAD256, HEAD96],
+                         ids=["small", "reference_small", "awkward", "odd", "split_mfma", "split_vector", "head64",
+                              "head256", "head96"])
 def test_chained_graph_is_bit_identical_to_ordinary(device, config):
     c = config
     initial, _ = oracle.make_inputs(c, 7, init="reference")
