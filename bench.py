@@ -15,6 +15,8 @@ Variants (run.py:24-38 plus two ablations):
                                         (the reference's inferred graph: branch concurrency only)
   contracted                            the inferred graph's contracted and merged launches
                                         captured on one stream (launch contraction only)
+  inferred_stream                       those launches issued on the stream, no graph (the cost
+                                        of submitting them as a graph)
   *_reuse                               the same with storage reuse on
   batched_*                             16 steps per graph submission (storage reuse on)
 
@@ -61,6 +63,7 @@ def log(*parts):
 def variants(steps):
     return [("sequential", False, "ordinary", 1), ("capture", False, "capture", 1), ("inferred", False, "graph", 1),
             ("branches", False, "branches", 1), ("contracted", False, "contracted", 1),
+            ("inferred_stream", False, "stream", 1),
             ("sequential_reuse", True, "ordinary", 1), ("capture_reuse", True, "capture", 1),
             ("inferred_reuse", True, "graph", 1), ("batched_capture", True, "capture", steps),
             ("batched_inferred", True, "graph", steps), ("batched_branches", True, "branches", steps)]

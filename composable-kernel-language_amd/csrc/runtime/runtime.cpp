@@ -19,10 +19,6 @@ int deviceCount() {
   return count;
 }
 
-bool inferredOnStream() {
-  const char *value = std::getenv("CKL_INFERRED_STREAM");
-  return value && std::strcmp(value, "1") == 0;
-}
 
 // ====================================================================== device and buffers
 static std::atomic<uint64_t> nextDeviceId{0};
@@ -495,7 +491,7 @@ void Invocation::validate(int mode, uint64_t batch) const {
   if (staticArena && staticEpochs[size_t(device->ordinal)].load() != epoch)
     throw std::invalid_argument("this invocation's static arena was taken over by a later ckl_bind_static on the same "
                                 "device; bind it again");
-  if (mode < kOrdinary || mode > kContractedCapture || !batch || plan.nodes.empty() ||
+  if (mode < kOrdinary || mode > kInferredStream || !batch || plan.nodes.empty() ||
       batch > 1000000 / plan.nodes.size())
     throw std::invalid_argument("invalid execution mode or batch exceeds one million kernel nodes");
 }
@@ -515,14 +511,20 @@ GraphExec &Invocation::graphFor(int mode, uint64_t batch) {
       slot = explicitGraph(repeated, units);
     } else {
       // Chains contracted, siblings of one family merged, units levelled by DAG depth; mode 1
-      // keeps the units' DAG as an explicit graph, mode 4 captures them as one launch chain.
+      // keeps the units' DAG as an explicit graph, mode 4 captures them as one launch chain and
+      // mode 5 keeps only the launch chain, issued on the stream at every execution.
       std::vector<Chain> chains = findChains(plan, temporaryResources);
       std::map<size_t, Launch> deferred = deferCombines(plan, temporaryResources, chains);
       std::vector<Unit> units = groupPlan(repeated, chains, deferred, batch);
       for (Unit &u : units) prepareParams(u.launch, *device);
       std::vector<Launch> launches;
       for (const Unit &u : units) launches.push_back(u.launch);
-      slot = mode == kInferred ? explicitGraph(repeated, units) : captureUnits(launches, stream);
+      if (mode == kInferred) slot = explicitGraph(repeated, units);
+      else if (mode == kContractedCapture) slot = captureUnits(launches, stream);
+      else {
+        slot = std::make_unique<GraphExec>();
+        slot->nodeCount = launches.size();
+      }
       slot->launches = std::move(launches);
       for (Unit &u : units) slot->members.push_back(std::move(u.members));
     }
@@ -537,7 +539,7 @@ void Invocation::execute(int mode, uint64_t batch) {
     return;
   }
   GraphExec &graph = graphFor(mode, batch);
-  if ((mode == kInferred || mode == kContractedCapture) && !graph.launches.empty() && inferredOnStream())
+  if (mode == kInferredStream)
     for (const Launch &l : graph.launches) launchOne(l, stream);
   else
     check(hipGraphLaunch(graph.exec, stream), "hipGraphLaunch");

@@ -29,7 +29,7 @@ namespace ckl::rt {
 
 void check(hipError_t status, const char *what);
 
-enum Mode { kOrdinary = 0, kInferred = 1, kCapture = 2, kBranches = 3, kContractedCapture = 4 };
+enum Mode { kOrdinary = 0, kInferred = 1, kCapture = 2, kBranches = 3, kContractedCapture = 4, kInferredStream = 5 };
 
 struct Device {
   explicit Device(int ordinal);
@@ -130,7 +130,7 @@ struct GraphExec {
   size_t nodeCount = 0;
   size_t edgeCount = 0;                        // dependency edges of an explicit graph
   std::vector<std::vector<uint8_t>> storage;   // kernarg blocks referenced during capture
-  std::vector<Launch> launches;                // contracted units in level order (modes 1 and 4)
+  std::vector<Launch> launches;                // contracted units in level order (modes 1, 4 and 5)
   std::vector<std::vector<size_t>> members;    // plan nodes each of those launches executes
   ~GraphExec();
 };
@@ -223,10 +223,6 @@ std::shared_ptr<Invocation> bind(const std::shared_ptr<ProgramState> &program, s
 // already resident on the device. Supersedes every earlier static binding on that device.
 std::shared_ptr<Invocation> bindStatic(const std::shared_ptr<ProgramState> &program, std::shared_ptr<Device> device,
                                        const std::vector<Argument> &arguments, hipStream_t stream);
-
-// CKL_INFERRED_STREAM=1: modes 1 and 4 issue the contracted launch chain as ordinary stream
-// launches instead of one graph launch (same kernels and order; for per-kernel profiling).
-bool inferredOnStream();
 
 int deviceCount();
 

@@ -2,13 +2,13 @@
 
 Binds the decode program (storage reuse on) to seeded synthetic state, sets the position to the
 configuration's prefill position (so attention covers context rows, as in the timed steps; the
-cache contents do not change kernel durations) and executes `--steps` inferred steps. With
-CKL_INFERRED_STREAM=1 in the environment the executor issues each step's launches on the stream
-instead of one graph launch, so a profiler sees every launch of the step (same kernels, same
-order). `--calibrate` adds four launches of the vector_pipeline `update` kernel, a copy of known
-size (4 MiB read, 4 MiB written), for scaling hardware byte counters.
+cache contents do not change kernel durations) and executes `--steps` inferred steps in mode
+"stream": the inferred graph's contracted launches issued on the stream, so a profiler sees every
+launch of the step (same kernels, same order as the graph). `--calibrate` adds four launches of
+the vector_pipeline `update` kernel, a copy of known size (4 MiB read, 4 MiB written), for scaling
+hardware byte counters.
 
-    CKL_INFERRED_STREAM=1 rocprofv3 --kernel-trace --stats -d out -- \\
+    rocprofv3 --kernel-trace --stats -d out -- \\
         python3 composable-kernel-language_amd/programs/profile_step.py --config large
 """
 from __future__ import annotations
@@ -44,7 +44,7 @@ def main() -> None:
     print(f"{args.config}: {inv.launch_count(mode='graph', batch_size=1)} launches per inferred step", flush=True)
     for _ in range(args.steps):
         state.reset(("position",))
-        inv.run(mode="graph", batch_size=1)
+        inv.run(mode="stream", batch_size=1)
     if args.calibrate:
         from programs import vector_pipeline as vp
         n = 1 << 20

@@ -284,10 +284,11 @@ class CompiledProgram(_Closable):
 class Invocation(_Closable):
     """A bound program: its stream, planned heaps and cached graphs."""
 
-    # The reference's three modes, plus two ablations of the inferred graph: "branches" is one
-    # graph node per dispatch with the reduced DAG's edges (the reference's inferred graph) and
-    # "contracted" captures the inferred graph's contracted launches on one stream.
-    MODES = {"ordinary": 0, "graph": 1, "capture": 2, "branches": 3, "contracted": 4}
+    # The reference's three modes, plus three variants of the inferred graph: "branches" is one
+    # graph node per dispatch with the reduced DAG's edges (the reference's inferred graph),
+    # "contracted" captures the inferred graph's contracted launches on one stream and "stream"
+    # issues those launches on the invocation stream with no graph.
+    MODES = {"ordinary": 0, "graph": 1, "capture": 2, "branches": 3, "contracted": 4, "stream": 5}
 
     def __init__(self, program, device, arguments, resource: _Handle):
         self.program, self.device, self.arguments = program, device, arguments

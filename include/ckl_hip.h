@@ -158,10 +158,12 @@ int ckl_bind_static(ckl_program *program, ckl_device *device, const ckl_argument
 uint64_t ckl_static_scratch_bytes(void);
 
 /* mode: 0 ordinary launches, 1 inferred graph, 2 single-stream capture (the reference's three,
- * lib/Runtime/NvidiaProgram.cpp:115-131), plus two ablations of mode 1 with no reference
+ * lib/Runtime/NvidiaProgram.cpp:115-131), plus three variants of mode 1 with no reference
  * counterpart as separate modes: 3 one kernel node per dispatch with the reduced DAG's edges (the
  * reference's own inferred graph, lib/Runtime/NvidiaRuntime.cpp:391-433: branch concurrency
- * only) and 4 mode 1's contracted and merged launches captured on one stream (contraction only).
+ * only), 4 mode 1's contracted and merged launches captured on one stream (contraction only) and
+ * 5 the same launches issued on the invocation stream at every run, with no graph (for profilers,
+ * and for plans of a few launches, where hipGraphLaunch's submission latency dominates).
  * Mode 1 is those contracted launches as an explicit graph with their DAG edges.
  * Synchronizes the invocation stream before returning. */
 int ckl_invocation_run(ckl_invocation *invocation, int mode, uint64_t batch);

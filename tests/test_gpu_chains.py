@@ -82,13 +82,13 @@ def test_chained_graph_is_bit_identical_to_ordinary(device, config):
             assert sum(n.startswith("ckl_linear_mfma") and n.endswith("_shared2") for n in names) == c.layers
         assert inv.launch_count(mode="graph", batch_size=c.steps) == c.steps * launches
         results = {}
-        for mode, group in (("ordinary", 1), ("graph", 1), ("graph", c.steps)):
+        for mode, group in (("ordinary", 1), ("graph", 1), ("graph", c.steps), ("stream", 1), ("stream", c.steps)):
             session.state.reset()
             for _ in range(c.steps // group):
                 inv.run(mode=mode, batch_size=group)
             session.state.verify(reference)
             results[(mode, group)] = {name: session.state.download(name) for name in MUTABLE}
-        for key in (("graph", 1), ("graph", c.steps)):
+        for key in (("graph", 1), ("graph", c.steps), ("stream", 1), ("stream", c.steps)):
             for name in MUTABLE:
                 assert np.array_equal(results[key][name], results[("ordinary", 1)][name]), (reuse, key, name)
 

@@ -16,7 +16,7 @@ REFERENCE_SMALL = Config(batch=1, hidden=64, heads=4, layers=2, ffn=128, vocab=2
 AWKWARD = Config(batch=3, hidden=48, heads=3, layers=1, ffn=80, vocab=129, context=3, steps=16)
 
 
-MODES = ("ordinary", "graph", "capture", "branches", "contracted")
+MODES = ("ordinary", "graph", "capture", "branches", "contracted", "stream")
 
 
 def run_and_check(device, c, init, steps, modes=MODES, groups=(1,)):
@@ -65,3 +65,5 @@ def test_branch_graph_is_the_reduced_dispatch_dag(device, name):
         assert inv.edge_count(mode="branches") == 24 * c.layers + 5
         assert inv.edge_count(mode="capture") == 0
         assert inv.launch_count(mode="contracted") == inv.launch_count(mode="graph")
+        assert inv.launch_count(mode="stream") == inv.launch_count(mode="graph")
+        assert inv.edge_count(mode="stream") == 0

@@ -27,7 +27,7 @@ def large(device):
 def test_large_one_step_all_modes(large):
     c, session, references = large
     for reuse, inv in session.invocations.items():
-        for mode in ("graph", "capture", "ordinary", "branches", "contracted"):
+        for mode in ("graph", "capture", "ordinary", "branches", "contracted", "stream"):
             session.state.reset()
             inv.run(mode=mode)
             assert session.state.verify(references[1], check_weights=False) < 2e-5, (reuse, mode)

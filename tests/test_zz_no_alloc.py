@@ -66,7 +66,7 @@ def check_against_ckl_bind(device, stream, c):
     session = DecoderSession(c, device, arrays=initial)     # ordinary binds: code objects now resident
     ordinary = session.invocations[True]
     handle = bind_static(session.programs[True], device, session.state.arguments(), stream)
-    for mode, name in ((0, "ordinary"), (1, "graph"), (2, "capture"), (3, "branches"), (4, "contracted")):
+    for mode, name in ((0, "ordinary"), (1, "graph"), (2, "capture"), (3, "branches"), (4, "contracted"), (5, "stream")):
         session.state.reset()
         ordinary.run(mode=name)
         expected = state(session)
