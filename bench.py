@@ -23,6 +23,10 @@ Variants (run.py:24-38 plus two ablations):
 --steps K is the number of decode steps timed per variant (ceil(K / 16) samples of one 16-step
 generation each); --warmup W the untimed warmup steps per variant. Neither changes the workload.
 
+Independent requests (`independent_requests`, small and wide): 8 invocations of one compiled
+program with shared weights, each on its own stream, bursts of one 16-step generation per request
+run side by side (ckl.run_requests), against the batching control (one invocation of 8 x B rows).
+
 Output: one JSON line on stdout; progress on stderr. The headline `value` is the large decoder's
 inferred-graph median µs/step (the largest single-GPU configuration of BASELINE.json). The CPU
 baseline (the NumPy restatement of the reference decoder step, oracle/decoder.py) runs in two
@@ -423,6 +427,71 @@ def cpu_baselines(directory: Path, workers, configs: dict, finals: dict) -> dict
     return out
 
 
+# ---------------------------------------------------------------------------- independent requests
+REQUESTS = 8
+REQUEST_RUNS = (("serial_inferred", "graph", 1, True), ("ordinary", "ordinary", 1, False),
+                ("capture", "capture", 1, False), ("inferred", "graph", 1, False),
+                ("inferred_group16", "graph", GENERATION, False), ("inferred_stream", "stream", 1, False))
+
+
+def independent_requests(device, names, samples):
+    """Independent requests (benchmarks/decoder/experiment.py:20-147; REPORT.md "Independent
+    requests and the batching control"): REQUESTS invocations of one compiled decode program with
+    shared weights and distinct prompts, GPU-prefilled, each timed 16-step generation burst run
+    side by side on their own streams (or one after another: serial_inferred); and the batching
+    control, one invocation of the same model with REQUESTS x B rows. Median burst wall and GPU
+    span over `samples` rotated/reversed bursts, tokens/s = requests x B x 16 / wall."""
+    from programs.decoder_config import CONFIGS, Config
+    from programs.harness import DecoderSession, RequestGroup, synthetic_inputs
+    out = {}
+    for name in names:
+        c = CONFIGS[name]
+        inputs = [synthetic_inputs(c, 123, prompt_seed=1000 + i) for i in range(REQUESTS)]
+        group = RequestGroup(c, device, [arrays for arrays, _ in inputs])
+        group.prefill([prompts for _, prompts in inputs])
+        rows = {label: {"wall_us": [], "span_us": []} for label, *_ in REQUEST_RUNS}
+        for label, mode, batch, serial in REQUEST_RUNS:          # warm: graphs built, clocks up
+            group.reset()
+            group.run(mode=mode, iterations=GENERATION // batch, batch_size=batch, serial=serial)
+        for sample in range(samples):
+            order = list(REQUEST_RUNS[sample % len(REQUEST_RUNS):] + REQUEST_RUNS[:sample % len(REQUEST_RUNS)])
+            for label, mode, batch, serial in (order if sample % 2 == 0 else reversed(order)):
+                group.reset()
+                t = group.run(mode=mode, iterations=GENERATION // batch, batch_size=batch, serial=serial)
+                rows[label]["wall_us"].append(t["wall_us"])
+                rows[label]["span_us"].append(t["span_us"])
+        tokens = REQUESTS * c.batch * GENERATION
+        result = {label: {"wall_ms": statistics.median(r["wall_us"]) / 1e3, "span_ms": statistics.median(r["span_us"]) / 1e3,
+                          "tokens_per_s": tokens / (statistics.median(r["wall_us"]) * 1e-6)}
+                  for label, r in rows.items()}
+        del group
+        # Batching control: the same model, REQUESTS x B rows in one invocation.
+        wide = Config(batch=REQUESTS * c.batch, hidden=c.hidden, heads=c.heads, layers=c.layers, ffn=c.ffn,
+                      vocab=c.vocab, context=c.context, steps=c.steps)
+        arrays, prompts = synthetic_inputs(wide, 123)
+        session = DecoderSession(wide, device, arrays=arrays)
+        session.prefill(prompts)
+        control = {}
+        for label, batch in (("batched_inferred", 1), ("batched_inferred_group16", GENERATION)):
+            inv = session.invocations[True]
+            session.state.reset()
+            inv.benchmark(iterations=GENERATION // batch, mode="graph", batch_size=batch)
+            runs = []
+            for _ in range(samples):
+                session.state.reset()
+                runs.append(inv.benchmark(iterations=GENERATION // batch, mode="graph", batch_size=batch))
+            wall = statistics.median(r["wall_us"] for r in runs) * GENERATION
+            control[label] = {"wall_ms": wall / 1e3,
+                              "span_ms": statistics.median(r["stream_us"] for r in runs) * GENERATION / 1e3,
+                              "tokens_per_s": tokens / (wall * 1e-6)}
+        del session
+        out[name] = {"requests": REQUESTS, "rows_per_request": c.batch, "steps": GENERATION,
+                     "independent": result, "batching_control": control}
+        log(f"[requests] {name}: " + "; ".join(f"{k} {v['wall_ms']:.3f} ms {v['tokens_per_s']:.0f} tok/s"
+                                               for k, v in {**result, **control}.items()))
+    return out
+
+
 # ---------------------------------------------------------------------------- vector pipeline
 def vector_pipeline(device, samples):
     """Config V: dst = (src + 0.5) + 0.5 over N = 1,048,576 f32 (examples/vector_pipeline.py),
@@ -441,7 +510,7 @@ def vector_pipeline(device, samples):
         compiled = {reuse: vp.lower(n).compile(fuse_pointwise=fuse, reuse_storage=reuse) for reuse in (False, True)}
         inv = compiled[True].bind(src, dst, 0.5)
         timing = {}
-        for mode in ("ordinary", "capture", "graph"):
+        for mode in ("ordinary", "capture", "graph", "stream"):
             inv.run(mode=mode)
             got = np.empty_like(x)
             dst.copy_to_host(got)
@@ -532,6 +601,7 @@ def measure(args, workdir, workers):
             save_state(workdir, name, session)
         del session
     vector = vector_pipeline(device, 7)
+    requests = independent_requests(device, [n for n in ("small", "wide") if n in args.configs], 7)
     cpu = cpu_baselines(workdir, workers, configs, finals) if workdir else {}
     for name, row in cpu.items():
         configs[name]["cpu_baseline"] = row
@@ -569,6 +639,7 @@ def measure(args, workdir, workers):
                                        "graph_setup_ms": vv["graph_setup_ms"]}
                                   for vn, vv in v["variants"].items()}} for k, v in configs.items()},
         "vector_pipeline": vector,
+        "independent_requests": requests,
         "host": host,
     }
     if args.output:

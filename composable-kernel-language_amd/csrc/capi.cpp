@@ -377,6 +377,23 @@ int ckl_invocation_benchmark(ckl_invocation *invocation, int mode, uint64_t iter
   });
 }
 
+int ckl_invocations_run(ckl_invocation *const *invocations, size_t count, int mode, uint64_t iterations,
+                        uint64_t batch, int serial, double out[2]) {
+  return guarded([&] {
+    require(invocations, "invocations");
+    std::vector<ckl::rt::Invocation *> requests;
+    for (size_t k = 0; k < count; ++k) {
+      require(invocations[k], "invocation");
+      requests.push_back(invocations[k]->invocation.get());
+    }
+    auto r = ckl::rt::runConcurrently(requests, mode, iterations, batch, serial != 0);
+    if (out) {
+      out[0] = r[0];
+      out[1] = r[1];
+    }
+  });
+}
+
 uint64_t ckl_invocation_node_count(ckl_invocation *invocation) {
   return invocation ? invocation->invocation->nodeCount() : 0;
 }

@@ -566,6 +566,67 @@ void Invocation::run(int mode, uint64_t batch) {
   check(hipStreamSynchronize(stream), "hipStreamSynchronize");
 }
 
+std::array<double, 2> runConcurrently(const std::vector<Invocation *> &requests, int mode, uint64_t iterations,
+                                      uint64_t batch, bool serial) {
+  if (requests.empty() || !iterations) throw std::invalid_argument("no requests or no iterations");
+  std::vector<Invocation *> order(requests);
+  std::sort(order.begin(), order.end());
+  if (std::adjacent_find(order.begin(), order.end()) != order.end())
+    throw std::invalid_argument("an invocation appears twice among the requests");
+  for (Invocation *r : order) {
+    if (!r) throw std::invalid_argument("null invocation among the requests");
+    if (r->device != order[0]->device) throw std::invalid_argument("requests on different devices");
+  }
+  // Locked in address order, so two bursts over overlapping sets cannot deadlock.
+  std::vector<std::unique_lock<std::mutex>> locks;
+  for (Invocation *r : order) locks.emplace_back(r->runMutex);
+  for (Invocation *r : requests) r->validate(mode, batch);
+  Device &device = *requests[0]->device;
+  device.makeCurrent();
+  for (Invocation *r : requests) {
+    check(hipStreamSynchronize(r->stream), "hipStreamSynchronize");
+    if (mode) r->graphFor(mode, batch);      // graphs built outside the timed burst
+  }
+  std::vector<hipEvent_t> events(requests.size() + 2, nullptr);
+  auto release = [&] {
+    for (hipEvent_t e : events)
+      if (e) hipEventDestroy(e);
+  };
+  try {
+    for (hipEvent_t &e : events) check(hipEventCreate(&e), "hipEventCreate");
+    hipStream_t first = requests[0]->stream;
+    using Clock = std::chrono::steady_clock;
+    auto wall = Clock::now();
+    check(hipEventRecord(events[0], first), "hipEventRecord");
+    for (size_t k = 1; k < requests.size(); ++k)
+      check(hipStreamWaitEvent(requests[k]->stream, events[0], 0), "hipStreamWaitEvent");
+    if (serial) {
+      for (size_t k = 0; k < requests.size(); ++k) {
+        for (uint64_t i = 0; i < iterations; ++i) requests[k]->execute(mode, batch);
+        check(hipStreamSynchronize(requests[k]->stream), "hipStreamSynchronize");
+      }
+    } else {
+      for (uint64_t i = 0; i < iterations; ++i)
+        for (Invocation *r : requests) r->execute(mode, batch);
+    }
+    for (size_t k = 1; k < requests.size(); ++k) {
+      check(hipEventRecord(events[k + 1], requests[k]->stream), "hipEventRecord");
+      check(hipStreamWaitEvent(first, events[k + 1], 0), "hipStreamWaitEvent");
+    }
+    check(hipEventRecord(events[1], first), "hipEventRecord");
+    check(hipEventSynchronize(events[1]), "hipEventSynchronize");
+    const double wallUs = std::chrono::duration<double, std::micro>(Clock::now() - wall).count();
+    float elapsed = 0;
+    check(hipEventElapsedTime(&elapsed, events[0], events[1]), "hipEventElapsedTime");
+    for (Invocation *r : requests) check(hipStreamSynchronize(r->stream), "hipStreamSynchronize");
+    release();
+    return {wallUs, double(elapsed) * 1000.0};
+  } catch (...) {
+    release();
+    throw;
+  }
+}
+
 std::array<double, 3> Invocation::benchmark(int mode, uint64_t iterations, uint64_t batch) {
   if (!iterations) throw std::invalid_argument("benchmark iterations must be positive");
   std::lock_guard<std::mutex> lock(runMutex);

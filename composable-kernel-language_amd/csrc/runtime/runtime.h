@@ -190,12 +190,22 @@ struct Invocation {
   std::vector<double> profileUnits(uint64_t repeats);
 
 private:
+  friend std::array<double, 2> runConcurrently(const std::vector<Invocation *> &, int, uint64_t, uint64_t, bool);
   void validate(int mode, uint64_t batch) const;
   GraphExec &inferredUnits();
   double timeLaunch(const Launch &launch, uint64_t iterations);
   GraphExec &graphFor(int mode, uint64_t batch);
   void execute(int mode, uint64_t batch);
 };
+
+// Independent requests: `iterations` executions of `batch` steps of every invocation in `mode`,
+// each on its own stream, submitted from this thread. Concurrent (`serial` false): step k of
+// every request is submitted before step k+1 of any, so the requests' launches run side by side;
+// serial: each request's executions complete before the next request starts. The invocations
+// must be distinct and on one device. Returns {host wall us, GPU span us} of the whole burst: the
+// span runs from an event that every stream waits for to one that waits for every stream.
+std::array<double, 2> runConcurrently(const std::vector<Invocation *> &requests, int mode, uint64_t iterations,
+                                      uint64_t batch, bool serial);
 
 using Entry = void (*)(void **);
 

@@ -23,12 +23,14 @@ LOGITS_NORMWISE = 1e-4
 WEIGHTS = ("emb", "norm1", "norm2", "final_norm", "wq", "wk", "wv", "wo", "wg", "wu", "wd", "lm")
 
 
-def synthetic_inputs(c: Config, seed: int = 123, *, init: str = "baseline"):
+def synthetic_inputs(c: Config, seed: int = 123, *, init: str = "baseline", prompt_seed: int = None):
     """Seeded weights, RoPE table, prompts and empty persistent state (no prefill).
 
     Draw order and distributions: weights in WEIGHTS order from default_rng(seed) (gains
     1 + N(0, 0.02); embedding and matrices N(0, 0.02) for init="baseline", or N(0, 0.5) and
-    N(0, 0.5/sqrt(fan_in)) for init="reference"), then prompts integers(0, V, (context, B)).
+    N(0, 0.5/sqrt(fan_in)) for init="reference"), then prompts integers(0, V, (context, B)) from
+    the same generator, or from default_rng(prompt_seed) when given (independent requests that
+    share the weights).
     """
     rng = np.random.default_rng(seed)
     sh = shapes(c)
@@ -46,7 +48,8 @@ def synthetic_inputs(c: Config, seed: int = 123, *, init: str = "baseline"):
     d, t = c.head_dim, c.capacity
     angles = np.arange(t)[:, None] * (10000. ** (-np.arange(0, d, 2) / d))[None, :]
     arrays["sincos"] = np.stack((np.cos(angles), np.sin(angles)), axis=-1).astype(np.float32)
-    prompts = rng.integers(0, c.vocab, (c.context, c.batch), dtype=np.int32)
+    prompt_rng = rng if prompt_seed is None else np.random.default_rng(prompt_seed)
+    prompts = prompt_rng.integers(0, c.vocab, (c.context, c.batch), dtype=np.int32)
     arrays.update(tokens=prompts[0].copy(), position=np.array([0], dtype=np.int32),
                   history=np.full(sh["history"][0], -1, dtype=np.int32),
                   kc=np.full(sh["kc"][0], SENTINEL, dtype=np.float32),
@@ -66,9 +69,11 @@ def normwise_error(actual: np.ndarray, reference: np.ndarray) -> float:
 
 
 class DecoderState:
-    """Device copies of every program argument, each followed by a sentinel tail."""
+    """Device copies of every program argument, each followed by a sentinel tail. With `shared`
+    (another request's state), the read-only inputs (weights, RoPE table) are that state's
+    buffers, which must hold the same values (benchmarks/decoder/run.py:81-101)."""
 
-    def __init__(self, device: ckl.Device, c: Config, arrays: dict):
+    def __init__(self, device: ckl.Device, c: Config, arrays: dict, *, shared: "DecoderState" = None):
         self.device, self.config = device, c
         self.initial = {k: v for k, v in arrays.items()}
         self.owners, self.buffers, self.host = {}, {}, {}
@@ -76,6 +81,12 @@ class DecoderState:
             values = arrays[name]
             if tuple(values.shape) != tuple(shape):
                 raise ValueError(f"{name}: shape {values.shape} != {shape}")
+            if shared is not None and name not in MUTABLE:
+                if not np.array_equal(values, shared.initial[name]):
+                    raise ValueError(f"cannot share different read-only input {name}")
+                self.owners[name], self.host[name] = shared.owners[name], shared.host[name]
+                self.buffers[name] = shared.buffers[name]
+                continue
             host = np.full(values.size + TAIL, SENTINEL, dtype=values.dtype)
             host[:values.size] = values.ravel()
             kind = ckl.i32 if dtype == "i32" else ckl.f32
@@ -190,3 +201,37 @@ class DecoderSession:
             if progress and (i + 1) % 128 == 0:
                 progress(i + 1, total)
         self.state.snapshot()
+
+
+class RequestGroup:
+    """Independent requests of one configuration (benchmarks/decoder/experiment.py:20-50): one
+    compiled decode program; the read-only weights and RoPE table allocated once and shared; per
+    request its own prompt and mutable state (tokens, position, history, caches, logits) and an
+    invocation with its own stream, heaps and workspaces."""
+
+    def __init__(self, c: Config, device: ckl.Device, arrays: list, *, reuse: bool = True):
+        self.config, self.device = c, device
+        self.states = []
+        for values in arrays:
+            self.states.append(DecoderState(device, c, values, shared=self.states[0] if self.states else None))
+        self.program = decode.lower(signature=signature(c)).compile(fuse_pointwise=False, reuse_storage=reuse)
+        self.invocations = [self.program.bind(*state.arguments()) for state in self.states]
+
+    def reset(self):
+        for state in self.states:
+            state.reset()
+
+    def run(self, *, mode="graph", iterations=1, batch_size=1, serial=False) -> dict:
+        return ckl.run_requests(self.invocations, mode=mode, iterations=iterations, batch_size=batch_size,
+                                serial=serial)
+
+    def prefill(self, prompts: list):
+        """Teacher-forced device prefill of every request (context-1 steps, the requests side by
+        side), then the prefilled state becomes each request's reset point."""
+        for i in range(self.config.context - 1):
+            self.run(mode="graph")
+            for state, p in zip(self.states, prompts):
+                state.set_tokens(p[i + 1])
+        for state in self.states:
+            state.snapshot()
+

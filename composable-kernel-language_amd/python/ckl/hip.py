@@ -307,7 +307,7 @@ class Invocation(_Closable):
         if graph:
             raise ValueError("specify either graph or mode")
         if mode not in cls.MODES:
-            raise ValueError("mode must be ordinary, graph, capture, branches, or contracted")
+            raise ValueError("mode must be ordinary, graph, capture, branches, contracted, or stream")
         return cls.MODES[mode]
 
     def _call(self, function, *args):
@@ -391,3 +391,23 @@ class Invocation(_Closable):
         out = (ctypes.c_double * 3)()
         self._call(_native.native().ckl_invocation_benchmark, execution, iterations, batch_size, out)
         return {"stream_us": out[0], "wall_us": out[1], "graph_setup_ms": out[2]}
+
+
+def run_requests(invocations, *, mode="graph", iterations=1, batch_size=1, serial=False) -> dict:
+    """Independent requests (benchmarks/decoder/experiment.py:53-70): `iterations` runs of
+    `batch_size` steps of every invocation in `mode`, each invocation on its own stream, submitted
+    from this thread; concurrently (step k of every request before step k+1 of any) or, with
+    `serial`, one request after another. The invocations may share read-only buffers; each owns
+    its stream, heaps and workspaces. Returns the burst's host wall and GPU span in microseconds."""
+    invocations = list(invocations)
+    if not invocations or not all(isinstance(i, Invocation) for i in invocations):
+        raise ValueError("run_requests takes one or more Invocation objects")
+    if type(iterations) is not int or not 0 < iterations < _MAX_U64:
+        raise ValueError("iterations must be a positive 64-bit count")
+    execution = Invocation._execution(False, mode, batch_size)
+    handles = (ctypes.c_void_p * len(invocations))(*[i._native_resource.pointer for i in invocations])
+    out = (ctypes.c_double * 2)()
+    _native.check(_native.native().ckl_invocations_run(handles, len(invocations), execution, iterations, batch_size,
+                                                       1 if serial else 0, out))
+    return {"wall_us": out[0], "span_us": out[1]}
+

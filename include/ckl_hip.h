@@ -170,6 +170,16 @@ int ckl_invocation_run(ckl_invocation *invocation, int mode, uint64_t batch);
 /* out[0] stream us/step, out[1] wall us/step, out[2] graph setup ms (NvidiaProgram.cpp:225-270). */
 int ckl_invocation_benchmark(ckl_invocation *invocation, int mode, uint64_t iterations, uint64_t batch, double out[3]);
 uint64_t ckl_invocation_node_count(ckl_invocation *invocation);
+/* Independent requests (replaces the thread-pool burst of benchmarks/decoder/experiment.py:53-70,
+ * one native benchmark call per request thread): `iterations` runs of `batch` steps of each of
+ * `count` distinct invocations of one device in `mode`, every invocation on its own stream, all
+ * submitted from the calling thread; with `serial` 0 step k of every request is submitted before
+ * step k+1 of any (the requests run side by side), otherwise each request completes before the
+ * next starts. Returns after every stream has finished. out (may be NULL): [0] host wall us of
+ * the burst, [1] its GPU span us (from an event every stream waits for to one that waits for
+ * every stream). */
+int ckl_invocations_run(ckl_invocation *const *invocations, size_t count, int mode, uint64_t iterations,
+                        uint64_t batch, int serial, double out[2]);
 /* Number of device launches (graph nodes) one execution of `batch` steps submits in `mode`. */
 int ckl_invocation_launch_count(ckl_invocation *invocation, int mode, uint64_t batch, uint64_t *count);
 /* Dependency edges of the explicit graph of `mode` (1 or 3; 0 for the other modes, whose
