@@ -359,6 +359,35 @@ int ckl_bind_static(ckl_program *program, ckl_device *device, const ckl_argument
 
 uint64_t ckl_static_scratch_bytes(void) { return CKL_STATIC_SCRATCH_BYTES; }
 
+namespace {
+// The ROCm tools extension's profiler control, looked up when first needed so that the library
+// does not depend on it: rocprofv3 --selected-regions records only what runs between a resume and
+// the following pause.
+using RoctxControl = int (*)(uint64_t);
+struct Roctx {
+  RoctxControl pause = nullptr, resume = nullptr;
+  Roctx() {
+    for (const char *name : {"librocprofiler-sdk-roctx.so.1", "librocprofiler-sdk-roctx.so"}) {
+      void *handle = dlopen(name, RTLD_NOW | RTLD_LOCAL);
+      if (!handle) continue;
+      pause = reinterpret_cast<RoctxControl>(dlsym(handle, "roctxProfilerPause"));
+      resume = reinterpret_cast<RoctxControl>(dlsym(handle, "roctxProfilerResume"));
+      if (pause && resume) return;
+      pause = resume = nullptr;
+    }
+  }
+};
+} // namespace
+
+int ckl_profiler_region(int active) {
+  return guarded([&] {
+    static Roctx roctx;
+    if (!roctx.pause) throw std::runtime_error("the ROCm tools extension (librocprofiler-sdk-roctx) is not available");
+    if ((active ? roctx.resume : roctx.pause)(0) != 0)
+      throw std::runtime_error(active ? "roctxProfilerResume failed" : "roctxProfilerPause failed");
+  });
+}
+
 int ckl_invocation_run(ckl_invocation *invocation, int mode, uint64_t batch) {
   return guarded([&] {
     require(invocation, "invocation");

@@ -411,3 +411,8 @@ def run_requests(invocations, *, mode="graph", iterations=1, batch_size=1, seria
                                                        1 if serial else 0, out))
     return {"wall_us": out[0], "span_us": out[1]}
 
+
+def profiler_region(active: bool) -> None:
+    """Resume (True) or pause (False) rocprofv3 collection under `--selected-regions`."""
+    _native.check(_native.native().ckl_profiler_region(1 if active else 0))
+

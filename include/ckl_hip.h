@@ -180,6 +180,11 @@ uint64_t ckl_invocation_node_count(ckl_invocation *invocation);
  * every stream). */
 int ckl_invocations_run(ckl_invocation *const *invocations, size_t count, int mode, uint64_t iterations,
                         uint64_t batch, int serial, double out[2]);
+/* Profiler region (replaces the CUDA profiler API range, cudaProfilerStart/Stop, that
+ * benchmarks/decoder/experiment.py:121-130 opens around one measured burst): 1 resumes and 0
+ * pauses collection through the ROCm tools extension (roctxProfilerResume/Pause), so
+ * `rocprofv3 --selected-regions` records only the region. Fails if that library is absent. */
+int ckl_profiler_region(int active);
 /* Number of device launches (graph nodes) one execution of `batch` steps submits in `mode`. */
 int ckl_invocation_launch_count(ckl_invocation *invocation, int mode, uint64_t batch, uint64_t *count);
 /* Dependency edges of the explicit graph of `mode` (1 or 3; 0 for the other modes, whose
