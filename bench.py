@@ -427,6 +427,40 @@ def cpu_baselines(directory: Path, workers, configs: dict, finals: dict) -> dict
     return out
 
 
+# ---------------------------------------------------------------------------- setup cost
+def setup_costs(session, samples=5):
+    """Host setup measured apart from steady-state decode (benchmarks/decoder/host_setup.py:17-77):
+    lowering and compilation (storage reuse off and on), a fresh bind, the first instantiation of
+    the inferred graph (one step and 16 steps per launch), and a rebind of the bound invocation
+    (ckl_invocation_rebind: argument addresses moved, the graph's kernel nodes updated in place,
+    no instantiation) with the graph launch after it. Medians over `samples`; the state is reset
+    afterwards."""
+    arguments = session.state.arguments()
+    out = {"lower_ms": session.lower_ms, "compile_ms": {str(k): v for k, v in session.compile_ms.items()}}
+    for reuse, program in session.programs.items():
+        rows = {k: [] for k in ("bind_ms", "graph_setup_ms", "graph16_setup_ms", "rebind_ms", "graph_after_rebind_setup_ms")}
+        for _ in range(samples):
+            start = time.perf_counter()
+            inv = program.bind(*arguments)
+            rows["bind_ms"].append((time.perf_counter() - start) * 1e3)
+            session.state.reset()
+            rows["graph_setup_ms"].append(inv.benchmark(iterations=1, mode="graph")["graph_setup_ms"])
+            session.state.reset()
+            rows["graph16_setup_ms"].append(inv.benchmark(iterations=1, mode="graph", batch_size=GENERATION)["graph_setup_ms"])
+            built = inv.graph_instantiations
+            start = time.perf_counter()
+            inv.rebind(*arguments)
+            rows["rebind_ms"].append((time.perf_counter() - start) * 1e3)
+            session.state.reset()
+            rows["graph_after_rebind_setup_ms"].append(inv.benchmark(iterations=1, mode="graph")["graph_setup_ms"])
+            if inv.graph_instantiations != built:
+                raise AssertionError("a rebind to buffers of the same layout re-instantiated the graph")
+            inv.close()
+        out[f"reuse_{'on' if reuse else 'off'}"] = {k: statistics.median(v) for k, v in rows.items()}
+    session.state.reset()
+    return out
+
+
 # ---------------------------------------------------------------------------- independent requests
 REQUESTS = 8
 REQUEST_RUNS = (("serial_inferred", "graph", 1, True), ("ordinary", "ordinary", 1, False),
@@ -596,6 +630,8 @@ def measure(args, workdir, workers):
                                      for k, v in summary.items()}
         result["roofline"] = roofline
         log(f"[{name}] dominant kernel {dominant}: {roofline}")
+        result["setup"] = setup_costs(session)
+        log(f"[{name}] setup: {result['setup']}")
         configs[name], finals[name] = result, final
         if workdir:
             save_state(workdir, name, session)

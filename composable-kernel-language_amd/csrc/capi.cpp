@@ -314,24 +314,30 @@ int ckl_buffer_copy_to_host(ckl_buffer *buffer, void *data, uint64_t bytes) {
 
 void ckl_buffer_release(ckl_buffer *buffer) { delete buffer; }
 
+namespace {
+std::vector<ckl::rt::Argument> convertArguments(const ckl_argument *arguments, size_t count) {
+  if (count && !arguments) throw std::invalid_argument("arguments must not be null");
+  std::vector<ckl::rt::Argument> args(count);
+  for (size_t k = 0; k < count; ++k) {
+    args[k].kind = arguments[k].kind;
+    if (arguments[k].kind == CKL_ARG_BUFFER) {
+      if (!arguments[k].buffer) throw std::invalid_argument("buffer argument must not be null");
+      args[k].buffer = arguments[k].buffer->buffer;
+    }
+    args[k].integer = arguments[k].integer;
+    args[k].real = arguments[k].real;
+  }
+  return args;
+}
+} // namespace
+
 int ckl_bind(ckl_program *program, ckl_device *device, const ckl_argument *arguments, size_t count,
              ckl_invocation **out) {
   return guarded([&] {
     require(program, "program");
     require(device, "device");
     require(out, "out");
-    if (count && !arguments) throw std::invalid_argument("arguments must not be null");
-    std::vector<ckl::rt::Argument> args(count);
-    for (size_t k = 0; k < count; ++k) {
-      args[k].kind = arguments[k].kind;
-      if (arguments[k].kind == CKL_ARG_BUFFER) {
-        if (!arguments[k].buffer) throw std::invalid_argument("buffer argument must not be null");
-        args[k].buffer = arguments[k].buffer->buffer;
-      }
-      args[k].integer = arguments[k].integer;
-      args[k].real = arguments[k].real;
-    }
-    *out = new ckl_invocation{ckl::rt::bind(program->state, device->device, args)};
+    *out = new ckl_invocation{ckl::rt::bind(program->state, device->device, convertArguments(arguments, count))};
   });
 }
 
@@ -420,6 +426,21 @@ int ckl_invocations_run(ckl_invocation *const *invocations, size_t count, int mo
       out[0] = r[0];
       out[1] = r[1];
     }
+  });
+}
+
+int ckl_invocation_rebind(ckl_invocation *invocation, const ckl_argument *arguments, size_t count) {
+  return guarded([&] {
+    require(invocation, "invocation");
+    invocation->invocation->rebind(convertArguments(arguments, count));
+  });
+}
+
+int ckl_invocation_graph_instantiations(ckl_invocation *invocation, uint64_t *count) {
+  return guarded([&] {
+    require(invocation, "invocation");
+    require(count, "count");
+    *count = invocation->invocation->graphInstantiations();
   });
 }
 

@@ -237,10 +237,6 @@ void launchOrdinary(const Plan &plan, hipStream_t stream) {
 // A unit of the inferred graph: one dispatch, a chain of dependent dispatches run by a chain
 // entry point, or sibling units of one family executed by the family's group entry point (each
 // member keeps its own grid range).
-struct Unit {
-  std::vector<size_t> members;
-  Launch launch;
-};
 
 // Group<Args> block of sibling launches. A shared-operand launch (`shared`) runs one member's grid
 // in which every workgroup serves all members; otherwise member m owns its own range of blocks.
@@ -444,6 +440,7 @@ std::unique_ptr<GraphExec> explicitGraph(const Plan &plan, const std::vector<Uni
     out->edgeCount += deps.size();
   }
   out->nodeCount = n;
+  out->handles = handles;
   check(hipGraphInstantiate(&out->exec, out->graph, nullptr, nullptr, 0), "hipGraphInstantiate");
   return out;
 }
@@ -496,38 +493,41 @@ void Invocation::validate(int mode, uint64_t batch) const {
     throw std::invalid_argument("invalid execution mode or batch exceeds one million kernel nodes");
 }
 
+// The units of a graph mode: ordinary launches (modes 2 and 3: one per dispatch) or the inferred
+// lowering (modes 1, 4 and 5: chains contracted, siblings of one family merged, units levelled by
+// DAG depth).
+std::vector<Unit> Invocation::buildUnits(int mode, uint64_t batch, const Plan &repeated) {
+  std::vector<Unit> units;
+  if (mode == kCapture || mode == kBranches) {
+    for (size_t k = 0; k < repeated.nodes.size(); ++k) units.push_back({{k}, repeated.nodes[k].launch});
+    return units;
+  }
+  std::vector<Chain> chains = findChains(plan, temporaryResources);
+  std::map<size_t, Launch> deferred = deferCombines(plan, temporaryResources, chains);
+  units = groupPlan(repeated, chains, deferred, batch);
+  for (Unit &u : units) prepareParams(u.launch, *device);
+  return units;
+}
+
 GraphExec &Invocation::graphFor(int mode, uint64_t batch) {
   auto &slot = graphs[{mode, batch}];
   if (!slot) {
     Plan repeated = batch == 1 ? plan : plan.repeat(batch);
-    if (mode == kCapture) {
-      std::vector<Launch> launches;
-      for (const PlanNode &n : repeated.nodes) launches.push_back(n.launch);
-      slot = captureUnits(launches, stream);
-    } else if (mode == kBranches) {
-      // The reference's inferred graph: one kernel node per dispatch, reduced DAG edges.
-      std::vector<Unit> units;
-      for (size_t k = 0; k < repeated.nodes.size(); ++k) units.push_back({{k}, repeated.nodes[k].launch});
-      slot = explicitGraph(repeated, units);
-    } else {
-      // Chains contracted, siblings of one family merged, units levelled by DAG depth; mode 1
-      // keeps the units' DAG as an explicit graph, mode 4 captures them as one launch chain and
-      // mode 5 keeps only the launch chain, issued on the stream at every execution.
-      std::vector<Chain> chains = findChains(plan, temporaryResources);
-      std::map<size_t, Launch> deferred = deferCombines(plan, temporaryResources, chains);
-      std::vector<Unit> units = groupPlan(repeated, chains, deferred, batch);
-      for (Unit &u : units) prepareParams(u.launch, *device);
-      std::vector<Launch> launches;
-      for (const Unit &u : units) launches.push_back(u.launch);
-      if (mode == kInferred) slot = explicitGraph(repeated, units);
-      else if (mode == kContractedCapture) slot = captureUnits(launches, stream);
-      else {
-        slot = std::make_unique<GraphExec>();
-        slot->nodeCount = launches.size();
-      }
-      slot->launches = std::move(launches);
-      for (Unit &u : units) slot->members.push_back(std::move(u.members));
+    std::vector<Unit> units = buildUnits(mode, batch, repeated);
+    std::vector<Launch> launches;
+    for (const Unit &u : units) launches.push_back(u.launch);
+    // Mode 3 is the reference's inferred graph (one kernel node per dispatch, reduced DAG edges)
+    // and mode 1 the units' DAG as an explicit graph; modes 2 and 4 capture their launch chain;
+    // mode 5 keeps only the launch chain, issued on the stream at every execution.
+    if (mode == kInferred || mode == kBranches) slot = explicitGraph(repeated, units);
+    else if (mode == kCapture || mode == kContractedCapture) slot = captureUnits(launches, stream);
+    else {
+      slot = std::make_unique<GraphExec>();
+      slot->nodeCount = launches.size();
     }
+    if (mode != kInferredStream) ++instantiations;
+    slot->launches = std::move(launches);
+    for (Unit &u : units) slot->members.push_back(std::move(u.members));
   }
   return *slot;
 }
@@ -624,6 +624,144 @@ std::array<double, 2> runConcurrently(const std::vector<Invocation *> &requests,
   } catch (...) {
     release();
     throw;
+  }
+}
+
+// The program arguments' device addresses (buffers, 0 for scalars) and scalar bytes, checked
+// against the compiled signature; the buffers are appended to `keep`.
+static void packArguments(const ProgramState &program, const Device *device, const std::vector<Argument> &arguments,
+                          std::vector<uint64_t> &addresses, std::vector<uint64_t> &scalars,
+                          std::vector<std::shared_ptr<Buffer>> &keep) {
+  const size_t count = arguments.size();
+  if (count != program.bufferBytes.size()) throw std::invalid_argument("incorrect program argument count");
+  addresses.assign(count, 0);
+  scalars.assign(count, 0);
+  for (size_t k = 0; k < count; ++k) {
+    const Argument &a = arguments[k];
+    if (program.bufferBytes[k]) {
+      if (a.kind != 0 || !a.buffer || a.buffer->device.get() != device || a.buffer->bytes < program.bufferBytes[k])
+        throw std::invalid_argument("buffer device or size does not match compiled signature");
+      addresses[k] = a.buffer->address();
+      keep.push_back(a.buffer);
+    } else {
+      const std::string &type = program.scalarTypes[k];
+      auto store = [&](auto value) { std::memcpy(&scalars[k], &value, sizeof(value)); };
+      if (type == "i32" && a.kind == 1) store(int32_t(a.integer));
+      else if (type == "i64" && a.kind == 2) store(int64_t(a.integer));
+      else if (type == "f32" && a.kind == 3) store(float(a.real));
+      else if (type == "f64" && a.kind == 4) store(double(a.real));
+      else throw std::invalid_argument("argument type does not match compiled signature");
+    }
+  }
+}
+
+// Whether any two buffer arguments' byte ranges overlap (the fused program's fallback condition,
+// lib/Runtime/NvidiaProgram.cpp:191-205).
+static bool argumentsOverlap(const ProgramState &program, const std::vector<uint64_t> &addresses) {
+  const size_t count = addresses.size();
+  for (size_t i = 0; i < count; ++i)
+    for (size_t j = i + 1; j < count; ++j) {
+      if (!program.bufferBytes[i] || !program.bufferBytes[j]) continue;
+      const bool overlap = addresses[i] <= addresses[j] ? addresses[j] - addresses[i] < program.bufferBytes[i]
+                                                        : addresses[i] - addresses[j] < program.bufferBytes[j];
+      if (overlap) return true;
+    }
+  return false;
+}
+
+static std::shared_ptr<Invocation> bindWith(const std::shared_ptr<ProgramState> &programIn, std::shared_ptr<Device> device,
+                                            const std::vector<Argument> &arguments, bool arena, hipStream_t stream);
+
+std::shared_ptr<Invocation> bind(const std::shared_ptr<ProgramState> &program, std::shared_ptr<Device> device,
+                                 const std::vector<Argument> &arguments) {
+  return bindWith(program, std::move(device), arguments, false, nullptr);
+}
+
+std::shared_ptr<Invocation> bindStatic(const std::shared_ptr<ProgramState> &program, std::shared_ptr<Device> device,
+                                       const std::vector<Argument> &arguments, hipStream_t stream) {
+  if (!device) throw std::invalid_argument("program binding requires a device");
+  if (!stream) throw std::invalid_argument("a no-allocation bind needs the caller's stream");
+  if (device->ordinal < 0 || device->ordinal >= kMaxStaticDevices)
+    throw std::invalid_argument("HIP device ordinal out of range for the static arena");
+  return bindWith(program, std::move(device), arguments, true, stream);
+}
+
+uint64_t Invocation::graphInstantiations() {
+  std::lock_guard<std::mutex> lock(runMutex);
+  return instantiations;
+}
+
+void Invocation::rebind(const std::vector<Argument> &arguments) {
+  std::lock_guard<std::mutex> lock(runMutex);
+  if (!requested) throw std::invalid_argument("this invocation was not bound from program arguments");
+  std::vector<uint64_t> addresses, scalars;
+  std::vector<std::shared_ptr<Buffer>> keep;
+  packArguments(*requested, device.get(), arguments, addresses, scalars, keep);
+  if (scalars != argumentScalars)
+    throw std::invalid_argument("a rebind keeps the scalar arguments; bind again to change them");
+  const bool fallback = requested->aliasFallback && argumentsOverlap(*requested, addresses);
+  if ((fallback ? requested->aliasFallback : requested) != program)
+    throw std::invalid_argument("the new buffers overlap differently (fused or unfused program); bind again");
+  for (int64_t k : resourceArgument)
+    if (k >= 0 && size_t(k) >= addresses.size()) throw std::logic_error("resource of an unknown argument");
+  // Move every resolved argument address by its buffer's displacement.
+  std::vector<uint64_t> delta(addresses.size());
+  for (size_t k = 0; k < addresses.size(); ++k) delta[k] = addresses[k] - argumentAddresses[k];
+  for (size_t id = 0; id < resourceArgument.size(); ++id)
+    if (resourceArgument[id] >= 0) resources[id] += delta[size_t(resourceArgument[id])];
+  for (PlanNode &node : plan.nodes) {
+    Launch &l = node.launch;
+    for (size_t s = 0; s < l.slotResources.size(); ++s) {
+      const int64_t id = l.slotResources[s];
+      if (id < 0 || size_t(id) >= resourceArgument.size() || resourceArgument[size_t(id)] < 0) continue;
+      if (l.slotSizes[s] != 8) throw std::logic_error("an address slot is not 8 bytes");
+      uint64_t value;
+      std::memcpy(&value, l.arguments.data() + l.slotOffsets[s], 8);
+      value += delta[size_t(resourceArgument[size_t(id)])];
+      std::memcpy(l.arguments.data() + l.slotOffsets[s], &value, 8);
+    }
+  }
+  argumentAddresses = addresses;
+  buffers = std::move(keep);
+  device->makeCurrent();
+  check(hipStreamSynchronize(stream), "hipStreamSynchronize");
+  // Explicit graphs: new unit launches from the moved plan; same structure -> update in place.
+  for (auto it = graphs.begin(); it != graphs.end();) {
+    const int mode = it->first.first;
+    const uint64_t batch = it->first.second;
+    GraphExec &g = *it->second;
+    bool kept = false;
+    if (mode == kInferredStream || ((mode == kInferred || mode == kBranches) && g.exec && g.handles.size() == g.launches.size())) {
+      Plan repeated = batch == 1 ? plan : plan.repeat(batch);
+      std::vector<Unit> units = buildUnits(mode, batch, repeated);
+      bool same = units.size() == g.launches.size();
+      for (size_t u = 0; same && u < units.size(); ++u) {
+        const Launch &a = units[u].launch, &b = g.launches[u];
+        same = a.function == b.function && a.shared == b.shared && units[u].members == g.members[u] &&
+               std::equal(a.grid, a.grid + 3, b.grid) && std::equal(a.block, a.block + 3, b.block);
+      }
+      if (same) {
+        if (mode != kInferredStream) {
+          g.storage.resize(units.size());
+          for (size_t u = 0; u < units.size(); ++u) {
+            const Launch &l = units[u].launch;
+            g.storage[u] = l.arguments;
+            Params params(l, g.storage[u].data());
+            hipKernelNodeParams p{};
+            p.func = reinterpret_cast<void *>(l.function);
+            p.gridDim = dim3(l.grid[0], l.grid[1], l.grid[2]);
+            p.blockDim = dim3(l.block[0], l.block[1], l.block[2]);
+            p.sharedMemBytes = l.shared;
+            p.kernelParams = params.at;
+            check(hipGraphExecKernelNodeSetParams(g.exec, g.handles[u], &p), "hipGraphExecKernelNodeSetParams");
+          }
+        }
+        for (size_t u = 0; u < units.size(); ++u) g.launches[u] = std::move(units[u].launch);
+        kept = true;
+      }
+    }
+    if (kept) ++it;
+    else it = graphs.erase(it);
   }
 }
 
@@ -780,65 +918,27 @@ static void appendArgument(Launch &launch, const void *data, uint64_t size, int6
   launch.slotResources.push_back(resource);
 }
 
-static std::shared_ptr<Invocation> bindWith(const std::shared_ptr<ProgramState> &programIn, std::shared_ptr<Device> device,
-                                            const std::vector<Argument> &arguments, bool arena, hipStream_t stream);
-
-std::shared_ptr<Invocation> bind(const std::shared_ptr<ProgramState> &program, std::shared_ptr<Device> device,
-                                 const std::vector<Argument> &arguments) {
-  return bindWith(program, std::move(device), arguments, false, nullptr);
-}
-
-std::shared_ptr<Invocation> bindStatic(const std::shared_ptr<ProgramState> &program, std::shared_ptr<Device> device,
-                                       const std::vector<Argument> &arguments, hipStream_t stream) {
-  if (!device) throw std::invalid_argument("program binding requires a device");
-  if (!stream) throw std::invalid_argument("a no-allocation bind needs the caller's stream");
-  if (device->ordinal < 0 || device->ordinal >= kMaxStaticDevices)
-    throw std::invalid_argument("HIP device ordinal out of range for the static arena");
-  return bindWith(program, std::move(device), arguments, true, stream);
-}
 
 static std::shared_ptr<Invocation> bindWith(const std::shared_ptr<ProgramState> &programIn, std::shared_ptr<Device> device,
                                             const std::vector<Argument> &arguments, bool arena, hipStream_t stream) {
   auto program = programIn;
   if (!device) throw std::invalid_argument("program binding requires a device");
-  size_t count = arguments.size();
-  if (count != program->bufferBytes.size()) throw std::invalid_argument("incorrect program argument count");
-  std::vector<uint64_t> addresses(count), scalars(count);
-  std::vector<void *> packed(count);
+  std::vector<uint64_t> addresses, scalars;
   std::vector<std::shared_ptr<Buffer>> buffers;
-  for (size_t k = 0; k < count; ++k) {
-    const Argument &a = arguments[k];
-    if (program->bufferBytes[k]) {
-      if (a.kind != 0 || !a.buffer || a.buffer->device != device || a.buffer->bytes < program->bufferBytes[k])
-        throw std::invalid_argument("buffer device or size does not match compiled signature");
-      addresses[k] = a.buffer->address();
-      packed[k] = &addresses[k];
-      buffers.push_back(a.buffer);
-    } else {
-      const std::string &type = program->scalarTypes[k];
-      auto store = [&](auto value) { std::memcpy(&scalars[k], &value, sizeof(value)); };
-      if (type == "i32" && a.kind == 1) store(int32_t(a.integer));
-      else if (type == "i64" && a.kind == 2) store(int64_t(a.integer));
-      else if (type == "f32" && a.kind == 3) store(float(a.real));
-      else if (type == "f64" && a.kind == 4) store(double(a.real));
-      else throw std::invalid_argument("argument type does not match compiled signature");
-      packed[k] = &scalars[k];
-    }
-  }
+  packArguments(*program, device.get(), arguments, addresses, scalars, buffers);
+  const size_t count = arguments.size();
+  std::vector<void *> packed(count);
+  for (size_t k = 0; k < count; ++k) packed[k] = program->bufferBytes[k] ? &addresses[k] : &scalars[k];
   // Fused programs fall back to their unfused form when external byte ranges overlap
   // (lib/Runtime/NvidiaProgram.cpp:191-205).
-  if (program->aliasFallback) {
-    bool overlap = false;
-    for (size_t i = 0; i < count; ++i)
-      for (size_t j = i + 1; j < count; ++j) {
-        if (!program->bufferBytes[i] || !program->bufferBytes[j]) continue;
-        overlap |= addresses[i] <= addresses[j] ? addresses[j] - addresses[i] < program->bufferBytes[i]
-                                                : addresses[i] - addresses[j] < program->bufferBytes[j];
-      }
-    if (overlap) program = program->aliasFallback;
-  }
+  if (program->aliasFallback && argumentsOverlap(*program, addresses)) program = program->aliasFallback;
   auto invocation = std::make_shared<Invocation>(program, device, stream);
   invocation->buffers = std::move(buffers);
+  invocation->requested = programIn;
+  invocation->argumentAddresses = addresses;
+  invocation->argumentScalars = scalars;
+  invocation->bindingAddresses = addresses.data();
+  invocation->bindingCount = count;
   if (arena) {
     invocation->staticArena = true;
     invocation->arenaBase = staticScratchAddress(device->ordinal);
@@ -850,6 +950,7 @@ static std::shared_ptr<Invocation> bindWith(const std::shared_ptr<ProgramState> 
   void **values = packed.data();
   void *entryArguments[] = {&frame, &values, program->entryContext};
   program->entry(entryArguments);
+  invocation->bindingAddresses = nullptr;
   if (!invocation->error.empty()) {
     // The reference reports callback failures as runtime errors; a program too large for the
     // static arena is the caller's argument error.
@@ -887,8 +988,15 @@ extern "C" void ckl_resource(void *frame, uint64_t id, uint64_t heap, uint64_t o
   ckl::rt::callback(frame, [&](Invocation &f) {
     if (f.resources.size() <= id) f.resources.resize(id + 1);
     if (f.temporaryResources.size() <= id) f.temporaryResources.resize(id + 1, false);
+    if (f.resourceArgument.size() <= id) f.resourceArgument.resize(id + 1, -1);
     f.temporaryResources[id] = !external;
-    if (external) f.resources[id] = *static_cast<uint64_t *>(external);
+    if (external) {
+      f.resources[id] = *static_cast<uint64_t *>(external);
+      // Which program argument the resource is: the entry passes the packed address's location.
+      const uint64_t *at = static_cast<const uint64_t *>(external);
+      if (f.bindingAddresses && at >= f.bindingAddresses && at < f.bindingAddresses + f.bindingCount)
+        f.resourceArgument[id] = at - f.bindingAddresses;
+    }
     else {
       const auto &h = f.heaps.at(heap);
       if (!h || offset > h->bytes) throw std::out_of_range("resource placement exceeds its heap");

@@ -96,6 +96,13 @@ struct Plan {
   Plan repeat(size_t iterations) const;      // roots of iteration i+1 follow every leaf of i
 };
 
+// One launch of a graph mode and the plan nodes it executes (one for ordinary units, several
+// for a contracted chain or a merged sibling group).
+struct Unit {
+  std::vector<size_t> members;
+  Launch launch;
+};
+
 // Dependent dispatches the inferred graph runs as one launch of a kernel-library chain entry
 // point (csrc/runtime/chains.cpp): `members` in dependency order, `launch` with the members'
 // argument blocks back to back. Found on one iteration of the plan; `temporary[id]` tells
@@ -130,12 +137,20 @@ struct GraphExec {
   size_t nodeCount = 0;
   size_t edgeCount = 0;                        // dependency edges of an explicit graph
   std::vector<std::vector<uint8_t>> storage;   // kernarg blocks referenced during capture
-  std::vector<Launch> launches;                // contracted units in level order (modes 1, 4 and 5)
+  std::vector<Launch> launches;                // the units in graph order (every mode but 2)
   std::vector<std::vector<size_t>> members;    // plan nodes each of those launches executes
+  std::vector<hipGraphNode_t> handles;         // kernel node of each unit (explicit graphs, modes 1 and 3)
   ~GraphExec();
 };
 
 struct ProgramState;
+
+struct Argument {
+  int kind = 0;                 // 0 buffer, 1 i32, 2 i64, 3 f32, 4 f64
+  std::shared_ptr<Buffer> buffer;
+  int64_t integer = 0;
+  double real = 0;
+};
 
 // Invocation: a bound program with its stream, heaps, resolved plan and cached graphs.
 struct Invocation {
@@ -165,10 +180,27 @@ struct Invocation {
   bool arenaExceeded = false;                       // the static arena was too small (bind fails)
   uint64_t carve(uint64_t bytes);                   // 256-aligned arena range for `bytes`
 
+  // The program arguments as bound: buffer addresses and scalar bytes; for each plan resource the
+  // program argument it is (-1: a heap placement); the program that was asked for (the bound one
+  // may be its unfused fallback). `bindingAddresses` is set while the host entry runs.
+  std::shared_ptr<ProgramState> requested;
+  std::vector<uint64_t> argumentAddresses, argumentScalars;
+  std::vector<int64_t> resourceArgument;
+  const uint64_t *bindingAddresses = nullptr;
+  size_t bindingCount = 0;
+  uint64_t instantiations = 0;                      // graph executables built for this invocation
+
   Invocation(std::shared_ptr<ProgramState> program, std::shared_ptr<Device> device, hipStream_t external = nullptr);
   ~Invocation();
   void run(int mode, uint64_t batch);
   std::array<double, 3> benchmark(int mode, uint64_t iterations, uint64_t batch);
+  // Rebinding without re-instantiation (NvidiaRuntime.cpp:466-496, updateKernel): the same
+  // program on other buffers of the same sizes (scalars unchanged). The plan's resolved argument
+  // addresses move; every cached explicit graph (modes 1 and 3) whose units keep their structure
+  // has its kernel nodes' parameters replaced in place (hipGraphExecKernelNodeSetParams); captured
+  // graphs and any graph whose units change are dropped and rebuilt at their next use.
+  void rebind(const std::vector<Argument> &arguments);
+  uint64_t graphInstantiations();
   size_t nodeCount() const { return plan.nodes.size(); }
   size_t graphNodeCount(int mode, uint64_t batch);
   size_t graphEdgeCount(int mode, uint64_t batch);
@@ -195,6 +227,7 @@ private:
   GraphExec &inferredUnits();
   double timeLaunch(const Launch &launch, uint64_t iterations);
   GraphExec &graphFor(int mode, uint64_t batch);
+  std::vector<Unit> buildUnits(int mode, uint64_t batch, const Plan &repeated);
   void execute(int mode, uint64_t batch);
 };
 
@@ -217,13 +250,6 @@ struct ProgramState {
   std::vector<std::string> scalarTypes;
   std::shared_ptr<ProgramState> aliasFallback;
   std::shared_ptr<void> owner;                      // keeps compiled state alive
-};
-
-struct Argument {
-  int kind = 0;                 // 0 buffer, 1 i32, 2 i64, 3 f32, 4 f64
-  std::shared_ptr<Buffer> buffer;
-  int64_t integer = 0;
-  double real = 0;
 };
 
 std::shared_ptr<Invocation> bind(const std::shared_ptr<ProgramState> &program, std::shared_ptr<Device> device,

@@ -317,6 +317,22 @@ class Invocation(_Closable):
         self._call(_native.native().ckl_invocation_run, self._execution(graph, mode, batch_size), batch_size)
         return self
 
+    def rebind(self, *arguments) -> "Invocation":
+        """The same program on other buffers of the same specs (scalars unchanged), keeping the
+        instantiated explicit graphs: their kernel nodes' parameters are updated in place."""
+        packed, _ = self.program._pack(arguments, self.device)
+        self._call(_native.native().ckl_invocation_rebind, packed, len(arguments))
+        self.arguments = arguments
+        return self
+
+    @property
+    def graph_instantiations(self) -> int:
+        """Graph executables built for this invocation so far (a rebind that updates nodes in
+        place adds none)."""
+        count = ctypes.c_uint64()
+        self._call(_native.native().ckl_invocation_graph_instantiations, ctypes.byref(count))
+        return int(count.value)
+
     @property
     def node_count(self) -> int:
         """Dispatches in the bound plan (including an overlap-triggered fallback)."""

@@ -170,6 +170,17 @@ int ckl_invocation_run(ckl_invocation *invocation, int mode, uint64_t batch);
 /* out[0] stream us/step, out[1] wall us/step, out[2] graph setup ms (NvidiaProgram.cpp:225-270). */
 int ckl_invocation_benchmark(ckl_invocation *invocation, int mode, uint64_t iterations, uint64_t batch, double out[3]);
 uint64_t ckl_invocation_node_count(ckl_invocation *invocation);
+/* Rebind without re-instantiation (NvidiaGraphExecutable::updateKernel, lib/Runtime/
+ * NvidiaRuntime.cpp:466-496, which updates one kernel node of an explicitly built graph): the
+ * invocation's program on other buffers of the same sizes, scalars unchanged. Every resolved
+ * argument address moves with its buffer; the cached explicit graphs (modes 1 and 3) whose units
+ * keep their structure get their kernel nodes' parameters replaced in place
+ * (hipGraphExecKernelNodeSetParams); captured graphs, and graphs whose chain decisions change with
+ * the new addresses, are rebuilt at their next run. Refused (invalid argument) when a scalar
+ * differs or the buffers overlap differently than at bind (fused vs unfused program). */
+int ckl_invocation_rebind(ckl_invocation *invocation, const ckl_argument *arguments, size_t count);
+/* Graph executables this invocation has instantiated so far (modes 1-4). */
+int ckl_invocation_graph_instantiations(ckl_invocation *invocation, uint64_t *count);
 /* Independent requests (replaces the thread-pool burst of benchmarks/decoder/experiment.py:53-70,
  * one native benchmark call per request thread): `iterations` runs of `batch` steps of each of
  * `count` distinct invocations of one device in `mode`, every invocation on its own stream, all
