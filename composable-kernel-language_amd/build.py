@@ -1,5 +1,6 @@
 """Build the native CKL backend in-tree: libckl_hip.so (host compiler pipeline, HIP executor,
-C ABI) and ckl_kernels_gfx950.hsaco (hand-written gfx950 kernel library).
+C ABI), ckl_kernels_gfx950.hsaco (hand-written gfx950 kernel library) and the ckl-opt
+command-line pass driver (linked against libckl_hip.so).
 
 Usage: python build.py [--jobs N]. Outputs go to python/ckl/_lib/.
 """
@@ -21,7 +22,7 @@ ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 ARCH = os.environ.get("CKL_OFFLOAD_ARCH", "gfx950")
 
 HOST_SOURCES = [
-    "core/ir.cpp", "core/planner.cpp", "core/analysis.cpp", "core/fusion.cpp", "core/compiler.cpp",
+    "core/ir.cpp", "core/planner.cpp", "core/analysis.cpp", "core/verify.cpp", "core/fusion.cpp", "core/compiler.cpp",
     "runtime/runtime.cpp", "runtime/chains.cpp", "runtime/codegen.cpp", "runtime/kernarg.cpp", "capi.cpp",
 ]
 KERNEL_SOURCES = ["kernels/library.hip"]
@@ -74,6 +75,16 @@ def build(jobs: int = 8) -> None:
     run(["g++", "-shared", "-o", str(tmp), *map(str, objects), f"-L{ROCM / 'lib'}",
          f"-Wl,-rpath,{ROCM / 'lib'}", "-lamdhip64", "-lhiprtc", "-ldl", "-pthread"])
     os.replace(tmp, library)
+    build_tool(library)
+
+
+def build_tool(library: Path) -> None:
+    """ckl-opt beside the library it links (found at run time through an $ORIGIN rpath)."""
+    tool = OUT / "ckl-opt"
+    tmp = tool.with_suffix(".tmp")
+    run(["g++", "-std=c++17", "-O2", "-Wall", str(CSRC / "tools" / "ckl_opt.cpp"), "-o", str(tmp),
+         f"-L{OUT}", "-l:" + library.name, "-Wl,-rpath,$ORIGIN"])
+    os.replace(tmp, tool)
 
 
 def build_kernels() -> None:

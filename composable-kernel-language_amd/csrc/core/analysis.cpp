@@ -169,6 +169,11 @@ void operationEffects(Op *op, std::vector<Effect> &effects, bool &modeled, bool 
   if (n == "ckl.free" || n == "memref.dealloc") { effects.push_back({Free, op->operands.empty() ? nullptr : op->operands[0]}); return; }
   if (n == "ckl.load" || n == "ckl.load_element" || n == "memref.load") { effects.push_back({Read, op->operands.at(0)}); return; }
   if (n == "ckl.store" || n == "ckl.store_element" || n == "memref.store") { effects.push_back({Write, op->operands.at(1)}); return; }
+  if (n == "memref.copy") {   // whole-buffer copy: reads its source, writes its target
+    effects.push_back({Read, op->operands.at(0)});
+    effects.push_back({Write, op->operands.at(1)});
+    return;
+  }
   if (n == "ckl.atomic_rmw") {
     effects.push_back({Read, op->operands.at(1)});
     effects.push_back({Write, op->operands.at(1)});
@@ -244,7 +249,7 @@ private:
   bool strict;
   std::set<const Op *> active;
 
-  static std::string where(const Op *op) { return op->loc.empty() ? std::string() : op->loc + ": "; }
+  static std::string where(const Op *op) { return sourcePosition(op); }
 
   static size_t argumentCount(const Op *function) {
     if (Block *entry = function->entry()) return entry->args.size();
@@ -648,8 +653,63 @@ std::optional<Graph> buildGraph(Module &module, Op *function, const std::map<con
   return graph;
 }
 
+// Argument descriptors of a dispatch node: what executable lowering will do with each argument
+// (resource packing with a view's byte range, constant, or host scalar argN), so that an
+// unsupported view or layout is visible in the graph before lowering rejects it.
+static Attr argumentDescriptors(const Op *dispatch, const Op *function, Namer &name) {
+  std::vector<Attr> out;
+  std::vector<Value *> actuals = dispatchArguments(dispatch);
+  for (size_t index = 0; index < actuals.size(); ++index) {
+    Value *argument = actuals[index];
+    std::vector<std::pair<std::string, Attr>> e = {{"index", Attr::integer(int64_t(index))},
+                                                   {"type", Attr::typeAttr(argument->type)}};
+    if (argument->type.isMemRef()) {
+      e.push_back({"kind", Attr::string("resource")});
+      e.push_back({"resource", Attr::string(name(argument))});
+      std::string packing = "direct_pointer";
+      if (getBaseResource(argument) != argument) {
+        if (auto range = staticResourceRange(argument)) {
+          e.push_back({"byte_offset", Attr::integer(range->offset)});
+          e.push_back({"byte_length", Attr::integer(range->length)});
+        } else {
+          packing = "unsupported_view";
+        }
+      } else if (!argument->type.identityLayout || argument->type.unranked) {
+        packing = "unsupported_layout";
+      }
+      e.push_back({"packing", Attr::string(packing)});
+    } else if (argument->def) {
+      if (const Attr *value = argument->def->attr("value")) {
+        e.push_back({"kind", Attr::string("constant")});
+        e.push_back({"value", *value});
+      } else {
+        e.push_back({"kind", Attr::string("unsupported")});
+      }
+    } else {
+      e.push_back({"kind", Attr::string(argument->owner == function->entry() ? "scalar" : "unsupported")});
+      e.push_back({"name", Attr::string("arg" + std::to_string(argument->index))});
+    }
+    out.push_back(Attr::dictOf(e));
+  }
+  return Attr::arrayOf(out);
+}
+
+static const Op *functionOf(const Op *op) {
+  for (const Op *p = op ? op->parentOp() : nullptr; p; p = p->parentOp())
+    if (p->name == "func.func") return p;
+  return nullptr;
+}
+
 std::string Graph::print() const {
   std::ostringstream out;
+  // Resource names as the lowering assigns them: allocations numbered by first use in node order.
+  const Op *function = nodes.empty() ? nullptr : functionOf(nodes.front().source);
+  std::optional<Namer> name;
+  if (function) {
+    name.emplace(function);
+    for (const GraphNode &node : nodes)
+      for (const BoundAccess &access : node.accesses) (*name)(access.resource);
+  }
   std::vector<Attr> resourceAttrs;
   for (const PlannedResource &r : resources) {
     std::vector<std::pair<std::string, Attr>> e = {
@@ -704,7 +764,12 @@ std::string Graph::print() const {
       if (const Attr *a = op->attr("implementation")) extra.push_back({"ckl.launch_implementation", *a});
       if (const Attr *a = op->attr("artifact") ? op->attr("artifact") : op->attr("implementation"))
         extra.push_back({"ckl.launch_artifact", *a});
-      if (const Attr *a = op->attr("capabilities")) extra.push_back({"ckl.launch_capabilities", *a});
+      if (const Attr *a = op->attr("capabilities")) {
+        extra.push_back({"ckl.launch_capabilities", *a});
+        for (const Attr &c : a->array)
+          if (c.s == "cuda.direct" || c.s == "rocm.bare_ptr") extra.push_back({"ckl.launch_abi", c});
+      }
+      if (name) extra.push_back({"ckl.arguments", argumentDescriptors(op, function, *name)});
     }
     out << "    \"ckl.graph_node\"() <" << Attr::dictOf(props).str() << "> " << Attr::dictOf(extra).str()
         << " : () -> ()\n";
@@ -763,7 +828,7 @@ Attr ExecArgument::attr() const {
   return Attr::dictOf(e);
 }
 
-static std::vector<uint8_t> littleEndian(const Attr &value, const Type &type) {
+std::vector<uint8_t> constantBytes(const Attr &value, const Type &type) {
   unsigned width = Type::bitWidth(type.kind);
   if (!width || width % 8 || width > 64) throw CompileError("host lowering requires byte-sized scalars up to 64 bits");
   uint64_t bits = 0;
@@ -861,9 +926,18 @@ void ExecPlan::verify() const {
         if (it == byName.end()) throw CompileError("'ckl_exec.kernel' op argument references an unknown resource");
         if (k.abi == "rocm.bare_ptr" && a.packing != "bare_pointer")
           throw CompileError("'ckl_exec.kernel' op rocm.bare_ptr resource arguments require bare_pointer packing");
+        if (k.abi == "cuda.direct" && a.packing != "direct_pointer")
+          throw CompileError("'ckl_exec.kernel' op cuda.direct resource arguments require direct_pointer packing");
         if (a.byteLength >= 0) {
+          // The range lies inside the resource, is as long as the argument's static identity-layout
+          // memref, and starts on an element boundary.
           int64_t bound = it->second->bytes;
-          if (a.byteOffset < 0 || a.byteLength <= 0 || a.byteOffset > bound || a.byteLength > bound - a.byteOffset)
+          const Type &t = a.type;
+          int64_t element = t.isMemRef() ? int64_t(Type::bitWidth(t.element) / 8) : 0;
+          bool typed = t.isMemRef() && t.hasStaticShape() && t.identityLayout && element > 0 &&
+                       Type::bitWidth(t.element) % 8 == 0 && t.elementCount() * element == a.byteLength;
+          if (a.byteOffset < 0 || a.byteLength <= 0 || a.byteOffset > bound || a.byteLength > bound - a.byteOffset ||
+              !typed || a.byteOffset % element)
             throw CompileError("'ckl_exec.kernel' op invalid or out-of-bounds resource byte range");
         }
       } else if (a.kind == "scalar") {
@@ -998,7 +1072,7 @@ ExecPlan lowerGraphToExec(const Module &module, const Op *function, const Graph 
       } else if (argument->def && argument->def->attr("value")) {
         a.kind = "constant";
         a.value = *argument->def->attr("value");
-        a.bytes = littleEndian(a.value, a.type);
+        a.bytes = constantBytes(a.value, a.type);
       } else if (!argument->def) {
         a.kind = "scalar";
         a.name = "arg" + std::to_string(argument->index);
@@ -1016,7 +1090,7 @@ ExecPlan lowerGraphToExec(const Module &module, const Op *function, const Graph 
         a.kind = "constant";
         a.type = c.type;
         a.value = c;
-        a.bytes = littleEndian(c, c.type);
+        a.bytes = constantBytes(c, c.type);
         k.arguments.push_back(std::move(a));
       }
     }

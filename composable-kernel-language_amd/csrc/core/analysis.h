@@ -161,6 +161,10 @@ struct ExecPlan {
 
 ExecPlan lowerGraphToExec(const Module &module, const Op *function, const Graph &graph);
 
+// Little-endian bytes of an integer or float constant of a byte-sized scalar type of at most
+// 64 bits, as the host passes it to a kernel argument slot.
+std::vector<uint8_t> constantBytes(const Attr &value, const Type &type);
+
 // -------------------------------------------------------------------- HIP preparation
 struct PrepareOptions {
   std::string chip = "gfx950";

@@ -1,8 +1,10 @@
 #include "compiler.h"
+#include "verify.h"
 
 #include "../runtime/callbacks.h"
 
 #include <cstdio>
+#include <set>
 #include <sstream>
 
 namespace ckl {
@@ -47,12 +49,13 @@ struct Sink {
   virtual void commit(uint64_t id) = 0;
 };
 
-void walkEntry(const CompiledProgram &program, Sink &sink, void **values) {
-  const ExecPlan &plan = program.plan;
+using ArtifactLookup = std::function<const Artifact *(const std::string &identity)>;
+
+void walkPlan(const ExecPlan &plan, const ArtifactLookup &artifacts, Sink &sink, void **values) {
   std::string current;
   auto select = [&](const std::string &identity) {
     if (identity == current) return;
-    const Artifact *a = program.artifact(identity);
+    const Artifact *a = artifacts(identity);
     if (!a) throw CompileError("executable plan references an unavailable artifact " + identity);
     sink.module(*a);
     current = identity;
@@ -93,6 +96,10 @@ void walkEntry(const CompiledProgram &program, Sink &sink, void **values) {
     for (int64_t d : k.dependencies) sink.dependency(uint64_t(d));
     sink.commit(uint64_t(k.id));
   }
+}
+
+void walkEntry(const CompiledProgram &program, Sink &sink, void **values) {
+  walkPlan(program.plan, [&](const std::string &identity) { return program.artifact(identity); }, sink, values);
 }
 
 struct CallbackSink : Sink {
@@ -141,6 +148,100 @@ struct TextSink : Sink {
   void commit(uint64_t id) override { out << "ckl_commit(" << id << ")\n"; }
 };
 
+// The host entry as IR: one "ckl_host.call" op per callback, in call order, inside a
+// "ckl_host.entry" op that names the plan and the host signature. Constant argument bytes are
+// kept exactly, as a string attribute (bytes outside printable ASCII print as \XX escapes).
+struct HostIRSink : Sink {
+  std::ostringstream out;
+  void call(const char *callee, std::vector<std::pair<std::string, Attr>> fields) {
+    fields.push_back({"callee", Attr::string(callee)});
+    out << "    \"ckl_host.call\"() <" << Attr::dictOf(std::move(fields)).str() << "> : () -> ()\n";
+  }
+  static Attr u64(uint64_t v) { return Attr::integer(int64_t(v)); }
+  void module(const Artifact &a) override { call("ckl_module", {{"artifact", Attr::string(a.identity)}}); }
+  void heap(uint64_t id, uint64_t bytes) override { call("ckl_heap", {{"id", u64(id)}, {"bytes", u64(bytes)}}); }
+  void resource(uint64_t id, uint64_t heap, uint64_t offset, int64_t argument) override {
+    if (argument >= 0) call("ckl_resource", {{"id", u64(id)}, {"argument", Attr::integer(argument)}});
+    else call("ckl_resource", {{"id", u64(id)}, {"heap", u64(heap)}, {"offset", u64(offset)}});
+  }
+  void kernel(const ExecKernel &k) override {
+    call("ckl_kernel", {{"entry_point", Attr::string(k.function)}, {"grid", Attr::denseI64(k.grid)},
+                        {"block", Attr::denseI64(k.block)}, {"shared_memory", Attr::integer(k.sharedMemory)}});
+  }
+  void argumentResource(uint64_t id, uint64_t offset) override {
+    call("ckl_argument_resource", {{"resource", u64(id)}, {"offset", u64(offset)}});
+  }
+  void argumentValue(const void *bytes, uint64_t size, const std::string &what) override {
+    if (!what.empty()) {
+      call("ckl_argument_value", {{"argument", Attr::integer(std::stoll(what.substr(3)))}, {"size", u64(size)}});
+    } else {
+      const char *p = static_cast<const char *>(bytes);
+      call("ckl_argument_value", {{"bytes", Attr::string(std::string(p, p + size))}, {"size", u64(size)}});
+    }
+  }
+  void workspace(uint64_t bytes) override { call("ckl_workspace", {{"bytes", u64(bytes)}}); }
+  void dependency(uint64_t id) override { call("ckl_dependency", {{"id", u64(id)}}); }
+  void commit(uint64_t id) override { call("ckl_commit", {{"id", u64(id)}}); }
+};
+
+// Checks that `plan` is a complete single-device HIP handoff for the native host entry
+// (the reference's host lowering, lib/Transforms/ExecToLLVM.cpp:122-190, requires the same of a
+// CUDA plan) and returns the host entry IR.
+std::string lowerPlanToHost(const Module &module, const ExecPlan &plan) {
+  if (plan.backend != "rocm") throw CompileError("host lowering requires the rocm backend, not '" + plan.backend + "'");
+  const Op *source = module.lookup(plan.source);
+  const Attr *results = source ? source->attr("ckl.num_results") : nullptr;
+  if (!source || source->name != "func.func" || (results && results->i != 0))
+    throw CompileError("host lowering requires a source function declaration with no results");
+  const std::vector<Type> &signature = plan.sourceArguments;
+  auto bound = [&](const std::string &name) -> const Type * {
+    if (name.size() <= 3 || name.rfind("arg", 0) != 0 || name.find_first_not_of("0123456789", 3) != std::string::npos)
+      return nullptr;
+    size_t index = std::stoul(name.substr(3));
+    return index < signature.size() ? &signature[index] : nullptr;
+  };
+  for (const ExecResource &r : plan.resources) {
+    if (r.device != "rocm:0") throw CompileError("host lowering requires rocm:0 resources, not '" + r.device + "'");
+    if (r.kind != "external") continue;
+    const Type *t = bound(r.name);
+    if (!t) throw CompileError("host lowering requires external resources bound to original argN arguments");
+    if (!t->isMemRef()) throw CompileError("external resource binding type does not match the source argument");
+  }
+  std::set<std::string> kernels;
+  for (const ExecKernel &k : plan.kernels) {
+    if (k.abi != "rocm.bare_ptr") throw CompileError("host lowering requires rocm.bare_ptr kernels, not '" + k.abi + "'");
+    if (k.device != "rocm:0") throw CompileError("host lowering requires rocm:0 kernels, not '" + k.device + "'");
+    kernels.insert(k.kernel.substr(0, k.kernel.find("::")));
+    for (const ExecArgument &a : k.arguments) {
+      if (a.kind != "scalar") continue;
+      const Type *t = bound(a.name);
+      if (!t) throw CompileError("host lowering requires original argN bindings within the source signature");
+      if (*t != a.type) throw CompileError("scalar binding type does not match the source argument");
+    }
+  }
+  // Device code is compiled separately: the host program holds the plan's source declaration
+  // and the kernels it launches, and nothing else.
+  for (auto &op : module.body()->ops) {
+    bool expected = op->name == "ckl_exec.plan" ||
+                    (op->name == "func.func" && (op->symName() == plan.source || kernels.count(op->symName())));
+    if (!expected) throw CompileError(sourcePosition(op.get()) + "host lowering found an unexpected operation '" + op->name + "'");
+  }
+  HostIRSink sink;
+  std::map<std::string, Artifact> stubs;
+  walkPlan(plan, [&](const std::string &identity) {
+    Artifact &a = stubs[identity];
+    a.identity = identity;
+    return &a;
+  }, sink, nullptr);
+  std::vector<Attr> arguments;
+  for (const Type &t : signature) arguments.push_back(Attr::typeAttr(t));
+  std::ostringstream out;
+  out << "  \"ckl_host.entry\"() <" << Attr::dictOf({{"arguments", Attr::arrayOf(arguments)}, {"name", Attr::string(plan.name)},
+                                                       {"source", Attr::string(plan.source)}}).str()
+      << "> ({\n" << sink.out.str() << "  }) : () -> ()\n";
+  return out.str();
+}
+
 std::string scalarName(const Type &t) {
   switch (t.kind) {
   case Type::I32: return "i32";
@@ -162,6 +263,7 @@ std::shared_ptr<CompiledProgram> compileProgram(const std::string &ir, const Com
                                                 const DeviceCompiler &deviceCompiler,
                                                 const std::function<Artifact()> &libraryArtifact) {
   auto module = parseModule(ir);
+  verifyModule(*module);
   if (module->op->attr("ckl.fusion.requires_disjoint"))
     throw CompileError("compile original source, not pre-fused guarded IR");
   bool fused = options.fusePointwise && fusePointwise(*module);
@@ -236,11 +338,18 @@ std::shared_ptr<CompiledProgram> compileProgram(const std::string &ir, const Com
 
 // ====================================================================== pass driver
 std::string runPasses(const std::string &ir, const std::vector<std::string> &passes) {
+  VerifyOptions verify;
+  std::vector<std::string> pipeline;
+  for (const std::string &spec : passes) {
+    if (spec == "allow-unregistered-dialect") verify.allowUnregisteredDialects = true;
+    else pipeline.push_back(spec);
+  }
   auto module = parseModule(ir);
+  verifyModule(*module, verify);
   std::vector<std::pair<Op *, Graph>> graphs;
   std::vector<ExecPlan> plans;
   std::map<const Op *, KernelSummary> summaries;
-  for (const std::string &spec : passes) {
+  for (const std::string &spec : pipeline) {
     std::string name = spec.substr(0, spec.find('{'));
     std::string options = spec.size() > name.size() ? spec.substr(name.size()) : std::string();
     auto has = [&](const char *option) { return options.find(option) != std::string::npos; };
@@ -260,6 +369,14 @@ std::string runPasses(const std::string &ir, const std::vector<std::string> &pas
       prepareHip(*module, {});
     } else if (name == "fuse-pointwise") {
       if (fusePointwise(*module)) module->op->attrs["ckl.fusion.requires_disjoint"] = Attr::unit();
+    } else if (name == "lower-exec-to-host") {
+      // Plans written in the input and plans lowered earlier in this pipeline, in that order.
+      if (&spec != &pipeline.back()) throw CompileError("lower-exec-to-host must be the last pass");
+      if (!graphs.empty()) throw CompileError("host lowering requires graphs lowered to executable plans first");
+      std::vector<ExecPlan> all = readExecPlans(*module);
+      all.insert(all.end(), plans.begin(), plans.end());
+      if (all.size() != 1) throw CompileError("host lowering requires exactly one executable plan");
+      return "module {\n" + lowerPlanToHost(*module, all.front()) + "}\n";
     } else {
       throw CompileError("unknown pass '" + name + "'");
     }

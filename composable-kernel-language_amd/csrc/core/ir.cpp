@@ -61,6 +61,7 @@ std::string Type::str() const {
     if (unranked) out += "*x";
     else for (int64_t d : shape) out += (d < 0 ? std::string("?") : std::to_string(d)) + "x";
     out += kindName(element);
+    if (!layout.empty()) out += ", " + layout;
     if (!memorySpace.empty()) out += ", " + memorySpace;
     return out + ">";
   }
@@ -134,8 +135,12 @@ std::string Attr::str() const {
   case Bool: return i ? "true" : "false";
   case Unit: return "unit";
   case Array: {
+    // As in MLIR's printer, an i64 integer directly inside an array is printed without its type.
     std::string out = "[";
-    for (size_t k = 0; k < array.size(); ++k) out += (k ? ", " : "") + array[k].str();
+    for (size_t k = 0; k < array.size(); ++k) {
+      const Attr &e = array[k];
+      out += (k ? ", " : "") + (e.kind == Int && e.type.kind == Type::I64 ? std::to_string(e.i) : e.str());
+    }
     return out + "]";
   }
   case DenseI64: case DenseI32: case DenseI8: {
@@ -180,6 +185,12 @@ Op *Module::lookup(const std::string &symbol) const {
   return nullptr;
 }
 
+std::string sourcePosition(const Op *op) {
+  if (!op->loc.empty()) return op->loc + ": ";
+  if (op->line) return std::to_string(op->line) + ":" + std::to_string(op->column) + ": ";
+  return {};
+}
+
 void walkPreOrder(Op *op, const std::function<void(Op *)> &fn) {
   fn(op);
   for (auto &region : op->regions)
@@ -192,7 +203,11 @@ namespace {
 
 class Parser {
 public:
-  explicit Parser(const std::string &text) : s(text) {}
+  explicit Parser(const std::string &text) : s(text) {
+    lineStarts.push_back(0);
+    for (size_t k = 0; k < s.size(); ++k)
+      if (s[k] == '\n') lineStarts.push_back(k + 1);
+  }
 
   std::unique_ptr<Module> parse() {
     auto module = std::make_unique<Module>();
@@ -229,11 +244,17 @@ private:
   size_t pos = 0;
   std::vector<std::unordered_map<std::string, Value *>> scopes;
 
+  std::vector<size_t> lineStarts;   // offset of the first character of each line
+
+  // 1-based line and column of a text offset.
+  std::pair<unsigned, unsigned> position(size_t offset) const {
+    offset = std::min(offset, s.size());
+    size_t line = size_t(std::upper_bound(lineStarts.begin(), lineStarts.end(), offset) - lineStarts.begin());
+    return {unsigned(line), unsigned(offset - lineStarts[line - 1] + 1)};
+  }
+
   [[noreturn]] void fail(const std::string &message) const {
-    size_t line = 1, column = 1;
-    for (size_t k = 0; k < pos && k < s.size(); ++k) {
-      if (s[k] == '\n') { ++line; column = 1; } else ++column;
-    }
+    auto [line, column] = position(pos);
     throw IRError(std::to_string(line) + ":" + std::to_string(column) + ": " + message);
   }
 
@@ -383,21 +404,27 @@ private:
       std::string elem = bareIdent();
       t.element = scalarKind(elem);
       if (t.element == Type::Opaque || t.element == Type::None) fail("unsupported element type " + elem);
-      if (consume(",")) {
+      // Optional layout, then optional memory space: memref<4xf32, strided<[1], offset: 4>, 3>.
+      while (consume(",")) {
         ws();
         size_t start = pos;
         int depth = 0;
-        while (pos < s.size() && !(depth == 0 && s[pos] == '>')) {
-          if (s[pos] == '<' || s[pos] == '(') ++depth;
-          if (s[pos] == '>' || s[pos] == ')') --depth;
+        while (pos < s.size() && !(depth == 0 && (s[pos] == '>' || s[pos] == ','))) {
+          if (s[pos] == '<' || s[pos] == '(' || s[pos] == '[') ++depth;
+          if (s[pos] == '>' || s[pos] == ')' || s[pos] == ']') --depth;
           ++pos;
         }
         std::string extra = s.substr(start, pos - start);
         while (!extra.empty() && std::isspace((unsigned char)extra.back())) extra.pop_back();
+        if (extra.empty()) fail("expected memref layout or memory space");
         if (extra.rfind("strided", 0) == 0 || extra.rfind("affine_map", 0) == 0) {
+          if (!t.layout.empty() || !t.memorySpace.empty()) fail("memref layout must precede the memory space");
           t.identityLayout = false;
+          t.layout = extra;
+        } else {
+          if (!t.memorySpace.empty()) fail("duplicate memref memory space");
           t.memorySpace = extra;
-        } else t.memorySpace = extra;
+        }
       }
       expect(">");
       return t;
@@ -605,6 +632,14 @@ private:
   void parseOperation(Block *block) {
     std::vector<std::string> names;
     ws();
+    auto [line, column] = position(pos);
+    parseOperationAt(block, names);
+    Op *op = block->ops.back().get();
+    op->line = line;
+    op->column = column;
+  }
+
+  void parseOperationAt(Block *block, std::vector<std::string> &names) {
     if (peek("%")) {
       do {
         std::string name = valueName();
@@ -799,6 +834,36 @@ private:
       expect("[");
       if (!consume("]")) { do raw->operands.push_back(operand()); while (consume(",")); expect("]"); }
       expect(":"); parseType();
+    } else if (n == "memref.copy") {
+      raw->operands.push_back(operand()); expect(",");
+      raw->operands.push_back(operand());
+      expect(":");
+      if (parseType() != raw->operands[0]->type) fail("memref.copy source type does not match its operand");
+      if (!keyword("to")) fail("expected 'to'");
+      if (parseType() != raw->operands[1]->type) fail("memref.copy target type does not match its operand");
+    } else if (n == "memref.subview") {
+      // Static offsets, sizes and strides only; kept in the attributes of MLIR's generic form.
+      raw->operands.push_back(operand());
+      auto staticList = [&](const char *key) {
+        expect("[");
+        std::vector<int64_t> values;
+        if (!consume("]")) {
+          do {
+            if (peek("%")) fail("memref.subview with dynamic offsets, sizes or strides is unsupported");
+            values.push_back(parseInteger());
+          } while (consume(","));
+          expect("]");
+        }
+        raw->attrs[key] = Attr::denseI64(values);
+      };
+      staticList("static_offsets");
+      staticList("static_sizes");
+      staticList("static_strides");
+      raw->attrs["operandSegmentSizes"] = Attr::denseI32({1, 0, 0, 0});
+      expect(":");
+      if (parseType() != raw->operands[0]->type) fail("memref.subview source type does not match its operand");
+      if (!keyword("to")) fail("expected 'to'");
+      results.push_back(parseType());
     } else if (n == "func.call") {
       raw->attrs["callee"] = Attr::symbol(symbolName());
       expect("(");

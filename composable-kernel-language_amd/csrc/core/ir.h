@@ -30,7 +30,8 @@ struct Type {
   Kind element = None;            // memref / vector element kind
   std::vector<int64_t> shape;     // -1 = dynamic extent
   bool unranked = false;          // memref<*xT>
-  bool identityLayout = true;     // non-identity layouts are kept as text only
+  bool identityLayout = true;     // false for strided<...> / affine_map<...> layouts
+  std::string layout;             // spelling of a non-identity layout, empty = identity
   std::string memorySpace;        // empty = default (global)
   std::string text;               // opaque spelling
 
@@ -117,6 +118,7 @@ struct Op {
   std::vector<std::unique_ptr<Region>> regions;
   Block *parent = nullptr;
   std::string loc;          // printed location, e.g. "file.py":12:3, empty = unknown
+  unsigned line = 0, column = 0;   // position in the parsed text (1-based), 0 = not parsed
 
   const Attr *attr(const std::string &key) const {
     auto it = attrs.find(key);
@@ -154,6 +156,10 @@ std::unique_ptr<Module> cloneModule(const Module &module);
 // the copies of results and block arguments are recorded in `map`.
 using ValueMap = std::unordered_map<const Value *, Value *>;
 std::unique_ptr<Op> cloneOp(const Op &op, Block *parent, ValueMap &map);
+
+// Diagnostic prefix naming where an op came from: its loc(...) when it has one, else its
+// "line:col" in the parsed text, followed by ": "; empty when neither is known.
+std::string sourcePosition(const Op *op);
 
 // Walk helpers.
 void walkPreOrder(Op *op, const std::function<void(Op *)> &fn);

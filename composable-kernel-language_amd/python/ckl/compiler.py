@@ -39,8 +39,10 @@ class CompiledModule:
 
 
 def compile_module(source: str, passes: Sequence[str] = ()) -> CompiledModule:
-    """Run native passes (summarize-effects, build-graph, lower-graph-to-exec, prepare-hip,
-    fuse-pointwise) over IR text in-process."""
+    """Verify IR text and run native passes over it in-process (summarize-effects, build-graph,
+    lower-graph-to-exec, prepare-hip, fuse-pointwise, lower-exec-to-host; options in braces, e.g.
+    "build-graph{strict=false}"; the item "allow-unregistered-dialect" admits unknown dialects).
+    The ckl-opt executable beside the native library runs the same pipeline from a command line."""
     from ._native import native_opt
     try:
         output = native_opt(source, list(passes))

@@ -66,8 +66,11 @@ int ckl_program_from_entry(void (*entry)(void **), const uint64_t *buffer_bytes,
                            size_t count, ckl_program *fallback, ckl_program **out);
 void ckl_program_release(ckl_program *program);
 
-/* ckl-opt style pass pipeline over IR text (tools/ckl-opt/ckl-opt.cpp:1-29): `passes` is a
- * comma-free list separated by ';', e.g. "build-graph;lower-graph-to-exec". */
+/* ckl-opt style pass pipeline over IR text (tools/ckl-opt/ckl-opt.cpp:1-29): `passes` is a list
+ * separated by ';', e.g. "build-graph{strict=false};lower-graph-to-exec". The input is verified
+ * first; the item "allow-unregistered-dialect" lets operations of unknown dialects through. Passes:
+ * summarize-effects, build-graph, lower-graph-to-exec, prepare-hip, fuse-pointwise and (last only)
+ * lower-exec-to-host. On success *out holds the printed module (free with ckl_string_free). */
 int ckl_opt(const char *ir, const char *passes, char **out);
 
 /* Storage planner (MemoryPlanner::plan, lib/Core/MemoryPlanner.cpp:98-204 and

@@ -169,11 +169,13 @@ UNKNOWN = '''module {
 
 
 def test_unknown_effects_strict_and_conservative():
-    with pytest.raises(RuntimeError, match="no complete memory-effect model"):
+    with pytest.raises(RuntimeError, match="unregistered dialect 'test'"):
         opt(UNKNOWN, "summarize-effects")
-    out = opt(UNKNOWN, "summarize-effects{strict=false}")
+    with pytest.raises(RuntimeError, match="no complete memory-effect model"):
+        opt(UNKNOWN, "allow-unregistered-dialect", "summarize-effects")
+    out = opt(UNKNOWN, "allow-unregistered-dialect", "summarize-effects{strict=false}")
     assert "unknown = true" in out and 'effects = ["read", "write"]' in out and "synchronizes = true" in out
-    edges = graph_edges(opt(UNKNOWN, "build-graph{strict=false}"))
+    edges = graph_edges(opt(UNKNOWN, "allow-unregistered-dialect", "build-graph{strict=false}"))
     assert "barrier" in edges[(2, 3)], "unknown dispatch did not order an otherwise independent dispatch"
 
 
@@ -253,7 +255,7 @@ def test_indexed_kernel_effects_and_plan():
     out = opt(INDEXED, "summarize-effects")
     update = out.split("func.func @update", 1)[1].split("func.func @first", 1)[0]
     assert 'effects = ["read"]' in update and 'effects = ["write"]' in update
-    assert 'region = "whole"' in update and "unknown = false" in update and "may_alias = [[0 : i64, 1 : i64]]" in update
+    assert 'region = "whole"' in update and "unknown = false" in update and "may_alias = [[0, 1]]" in update
     first = out.split("func.func @first", 1)[1].split("func.func @step", 1)[0]
     assert "effects = [\"read\", \"write\"], region = {length = 12 : i64, offset = 0 : i64}" in first
     edges = graph_edges(opt(INDEXED, "build-graph"))
