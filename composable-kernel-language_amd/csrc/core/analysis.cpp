@@ -1193,6 +1193,31 @@ std::string prepareHip(Module &module, const PrepareOptions &options) {
       dispatch->attrs["ckl.hip.entry_point"] = *entry;
       for (const char *key : {"grid", "block", "shared_memory", "constants", "group", "workspace"})
         if (const Attr *a = chosen->get(key)) dispatch->attrs[std::string("ckl.hip.") + key] = *a;
+      if (const Attr *variants = chosen->get("variants")) {
+        // Siblings: dispatches of this kernel in the same block whose first operand is the same
+        // value (the inferred graph runs them as one shared-operand launch). The variant for the
+        // most members not above their count replaces the launch, in every run mode alike.
+        int64_t siblings = 0;
+        for (auto &op : dispatch->parent->ops)
+          if (op->name == "ckl.dispatch" && symbolOf(op.get(), "kernel") == symbol && !op->operands.empty() &&
+              !dispatch->operands.empty() && op->operands[0] == dispatch->operands[0])
+            ++siblings;
+        const Attr *best = nullptr;
+        int64_t bestMembers = 0;
+        for (const Attr &v : variants->array) {
+          const Attr *members = v.get("members");
+          if (!members || members->kind != Attr::Int) throw CompileError("library selection variant for " + symbol + " is incomplete");
+          if (members->i <= siblings && members->i > bestMembers) {
+            best = &v;
+            bestMembers = members->i;
+          }
+        }
+        if (best) {
+          if (const Attr *e = best->get("entry_point")) dispatch->attrs["ckl.hip.entry_point"] = *e;
+          for (const char *key : {"grid", "block", "shared_memory", "constants", "workspace"})
+            if (const Attr *a = best->get(key)) dispatch->attrs[std::string("ckl.hip.") + key] = *a;
+        }
+      }
     } else {
       dispatch->attrs["artifact"] = Attr::string(artifact);
       dispatch->attrs["implementation"] = Attr::string(artifact + "." + symbol);

@@ -48,6 +48,11 @@ class Launch:
     shared: int = 0
     entry: str = ""          # entry point when the family has several (default ckl_<name>)
     workspace: int = 0       # private zero-initialised device workspace bytes (ckl_workspace)
+    # (members, Launch): the launch a dispatch takes instead when at least `members` dispatches
+    # of the kernel in its block multiply the same first operand (siblings the inferred graph
+    # runs as one shared-operand launch); the native prepare step picks it per dispatch, so every
+    # run mode launches the same tiling.
+    variants: tuple = ()
 
 
 def _elementwise(count: int, inner: int) -> int:
@@ -91,6 +96,12 @@ def _rms_apply(shapes, consts, ext):
 # (B <= 16, latency-bound) runs one workgroup per (64-column tile, batch row) whose up to 16
 # waves take 64 reduction rows each, all loaded in one round trip; it splits only beyond 1024
 # rows.
+# Three or more siblings (q/k/v) try J = 1 first: each member then contributes 2 KB to a wave's
+# stage (6 KB for three), and the grid of the same size splits K into half as many slices, so
+# the launch writes half the partial planes and its consumer adds half as many. Measured on the
+# large decoder's projections alone (cold weights, in sequence): q/k/v 14.7 us with J = 1 against
+# 16.1-16.4 us with J = 2, while a single projection of the same shape is slower with J = 1
+# (6.5 us against 7.2 us) and the gate/up pair is no faster with J = 2 (24.2 against 24.4 us).
 LINEAR_TARGET_GROUPS = 256    # MI355X compute units
 LINEAR_MIN_FILL = 0.85
 LINEAR_MIN_CHUNK = 256
@@ -100,11 +111,16 @@ LINEAR_VECTOR_WAVES = 16      # waves per vector-path workgroup at most (1024 th
 LINEAR_VECTOR_WAVE_ROWS = 64  # kVectorRows: reduction rows per wave
 
 
-def linear_tiling(b: int, i: int, o: int) -> dict:
+LINEAR_SHARED_J1_MEMBERS = 3   # siblings from which the MFMA path tries J = 1 first
+
+
+def linear_tiling(b: int, i: int, o: int, members: int = 1) -> dict:
+    """Tiling of one linear (`members` = how many sibling linears of this shape multiply the same
+    x and run as one shared-operand launch)."""
     if b > LINEAR_VECTOR_ROWS and i % 4 == 0 and o % 4 == 0:
         row_tiles = _cdiv(b, 32)
         best = None
-        for j in (2, 4, 1):
+        for j in ((1, 2, 4) if members >= LINEAR_SHARED_J1_MEMBERS else (2, 4, 1)):
             tiles = _cdiv(o, 32 * j)
             split = max(1, min(LINEAR_TARGET_GROUPS // (row_tiles * tiles), i // LINEAR_MIN_CHUNK))
             chunk = _cdiv(_cdiv(i, split), 16) * 16
@@ -145,11 +161,16 @@ def _linear(shapes, consts, ext):
     layer = consts[3]
     if not (0 <= layer < w) or not (ext[0] >= o and ext[1:] == (b, 1)):
         return None
+    def launch(t, variants=()):
+        return Launch(t["grid"], (b, i, o, layer, t["tiles"], t["split"], t["chunk"], 0), block=t["block"],
+                      shared=t["shared"], entry=t["entry"], workspace=t["workspace"], variants=variants)
+
     t = linear_tiling(b, i, o)
     if t is None:
         return None
-    return Launch(t["grid"], (b, i, o, layer, t["tiles"], t["split"], t["chunk"], 0), block=t["block"],
-                  shared=t["shared"], entry=t["entry"], workspace=t["workspace"])
+    shared = linear_tiling(b, i, o, LINEAR_SHARED_J1_MEMBERS)
+    variants = ((LINEAR_SHARED_J1_MEMBERS, launch(shared)),) if shared != t else ()
+    return launch(t, variants)
 
 
 def _rope(shapes, consts, ext):
@@ -327,6 +348,16 @@ def selection_attribute(selections: dict, artifact: str) -> str:
                   f'implementation = "ckl.hip.library.{s.kernel.name}"', f"shared_memory = {s.launch.shared} : i64"]
         if s.launch.workspace:
             fields.append(f"workspace = {s.launch.workspace} : i64")
+        if s.launch.variants:
+            variants = []
+            for members, v in s.launch.variants:
+                variant = [f"block = array<i64: {v.block}, 1, 1>",
+                           "constants = [" + ", ".join(f"{int(c)} : i32" for c in v.constants) + "]",
+                           f'entry_point = "{v.entry or s.kernel.entry_point}"', f"grid = array<i64: {v.grid}, 1, 1>",
+                           f"members = {members} : i64", f"shared_memory = {v.shared} : i64",
+                           f"workspace = {v.workspace} : i64"]
+                variants.append("{" + ", ".join(variant) + "}")
+            fields.append("variants = [" + ", ".join(variants) + "]")
         if s.kernel.groupable:
             fields.append(f'group = "{s.kernel.name}"')
         entries.append(f"{symbol} = {{{', '.join(sorted(fields))}}}")

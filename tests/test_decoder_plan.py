@@ -111,3 +111,28 @@ def test_decoder_offsets_match_reference_planner(name):
         assert len(mine) == len(resources)
         for k, r in enumerate(resources):
             assert mine[r["name"]] == ref_offsets[k], (reuse, r["name"])
+
+
+def test_sibling_linears_take_their_shared_tiling():
+    """The three linears that multiply one x (q, k, v) get the tiling chosen for three siblings in
+    every run mode (the prepare step picks the selection's variant per dispatch); o, of the same
+    shape and layer but with its own x, keeps the single-linear tiling; gate/up (two siblings) and
+    the other projections are unchanged."""
+    from ckl.library import linear_tiling
+    c = CONFIGS["large"]
+    ir = decode.lower(signature=signature(c)).compile(fuse_pointwise=False).executable_ir
+    launches = {}
+    for line in ir.splitlines():
+        if '"ckl_exec.kernel"' in line and "ckl_linear_" in line:
+            key = (re.search(r'entry_point = "([^"]+)"', line).group(1), int(re.search(r"\bgrid = array<i64: (\d+)", line).group(1)))
+            launches[key] = launches.get(key, 0) + 1
+    single = linear_tiling(c.batch, c.hidden, c.hidden)
+    siblings = linear_tiling(c.batch, c.hidden, c.hidden, members=3)
+    assert siblings["entry"] == "ckl_linear_mfma1x1" and siblings["split"] < single["split"] and single["entry"] == "ckl_linear_mfma2x1"
+    gate_up = linear_tiling(c.batch, c.hidden, c.ffn)
+    down = linear_tiling(c.batch, c.ffn, c.hidden)
+    head = linear_tiling(c.batch, c.hidden, c.vocab)
+    expected = {}
+    for t, n in ((siblings, 3 * c.layers), (single, c.layers), (gate_up, 2 * c.layers), (down, c.layers), (head, 1)):
+        expected[(t["entry"], t["grid"])] = expected.get((t["entry"], t["grid"]), 0) + n
+    assert launches == expected
