@@ -4,7 +4,8 @@ Binds the decode program (storage reuse on) to seeded synthetic state, sets the 
 configuration's prefill position (so attention covers context rows, as in the timed steps; the
 cache contents do not change kernel durations) and executes `--steps` inferred steps in mode
 "stream": the inferred graph's contracted launches issued on the stream, so a profiler sees every
-launch of the step (same kernels, same order as the graph). `--calibrate` adds four launches of
+launch of the step (same kernels, same order as the graph; `--mode graph` runs the graph itself,
+to compare the two on the GPU clock). `--calibrate` adds four launches of
 the vector_pipeline `update` kernel, a copy of known size (4 MiB read, 4 MiB written), for scaling
 hardware byte counters.
 
@@ -29,6 +30,8 @@ def main() -> None:
     parser.add_argument("--config", default="large")
     parser.add_argument("--steps", type=int, default=12)
     parser.add_argument("--calibrate", action="store_true")
+    parser.add_argument("--mode", default="stream", choices=("stream", "graph"),
+                        help="stream: the launches one by one; graph: the same launches as one hipGraph per step")
     args = parser.parse_args()
 
     import ckl
@@ -44,7 +47,7 @@ def main() -> None:
     print(f"{args.config}: {inv.launch_count(mode='graph', batch_size=1)} launches per inferred step", flush=True)
     for _ in range(args.steps):
         state.reset(("position",))
-        inv.run(mode="stream", batch_size=1)
+        inv.run(mode=args.mode, batch_size=1)
     if args.calibrate:
         from programs import vector_pipeline as vp
         n = 1 << 20
