@@ -50,6 +50,13 @@ struct CKL_ALIGN LinearArgs {
 // partial planes float[kSplit][rows][O], rows = B for the vector path (ckl_linear_rowvec) and
 // 32 * ceil(B / 32) for the MFMA paths.
 constexpr int kLinearZeroPage = 256;
+// The MFMA linear's epilogue hands the accumulators of EM members through LDS in one pass:
+// 16 KB per member and weight column of a lane (4 waves x 16 registers x 64 lanes x 4 bytes), at
+// most kLinearEpilogueBytes; a shared-operand launch of more members takes them EM at a time.
+constexpr int kLinearEpilogueBytes = 128 * 1024;
+constexpr int linearEpilogueMembers(int M, int J) {
+  return M * J * 16384 <= kLinearEpilogueBytes ? M : (kLinearEpilogueBytes / (J * 16384) > 0 ? kLinearEpilogueBytes / (J * 16384) : 1);
+}
 constexpr uint64_t linearCounterBytes(uint64_t counters) { return (counters * 4 + 255) & ~uint64_t(255); }
 constexpr uint64_t linearPlaneRows(int B, bool vector) { return vector ? uint64_t(B) : uint64_t((B + 31) / 32) * 32; }
 constexpr uint64_t linearPartialsOffset(int B, int tilesN, bool vector) {

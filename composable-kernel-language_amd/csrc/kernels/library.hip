@@ -606,6 +606,12 @@ template <int J, bool NT> __device__ __forceinline__ void load_columns(float (&o
   }
 }
 
+template <int J> __device__ __forceinline__ void store_columns(float *p, const float (&v)[J]) {
+  if constexpr (J == 4) *reinterpret_cast<float4 *>(p) = make_float4(v[0], v[1], v[2], v[3]);
+  else if constexpr (J == 2) *reinterpret_cast<float2 *>(p) = make_float2(v[0], v[1]);
+  else *p = v[0];
+}
+
 // One stage = 16*S reduction rows of one lane (2S 8-row super-steps): x[row][k+8u .. k+8u+3] and
 // the lane's J weight columns of rows k+8u+i. Full stages load without predicates or selects, so
 // the next stage's loads stay in flight under the current stage's MFMAs: a batch row >= B (x row
@@ -733,56 +739,68 @@ __device__ void linear_mfma(const LinearArgs *a, int block, float *smem) {
     mfma_compute<J, 1, M>(st, acc);
   }
 
-  // Every wave hands its tile to the others through LDS; wave w then adds rows {8w + 4s + q} of
-  // the tile (its accumulator registers 4w .. 4w+3) in wave order and stores them, so the four
-  // waves share the epilogue. Columns go through LDS in groups of JH (at most 2: 32 KB), member
-  // after member. Partial planes the consumer combines (deferred) are plain stores; planes
-  // combined here go through the agent-coherent path.
-  constexpr int JH = J < 2 ? J : 2;
+  // Every wave hands its accumulators to the others through LDS in one pass (EM members at a
+  // time, one float4 per lane and register quad); wave w then adds, for each member and column,
+  // the four waves' quads 4w .. 4w+3 (its rows {8w + 4s + q}) in wave order and stores the lane's
+  // J columns of each row with one vector store, so the four waves share the epilogue. Partial
+  // planes the consumer combines (deferred) are plain stores; planes combined here go through
+  // the agent-coherent path. `smem` is 16-byte aligned: float4 LDS accesses at an offset of 4
+  // (after a 4-byte static variable) are split by the hardware and cost more than the pass saves.
+  constexpr int EM = linearEpilogueMembers(M, J);
   const int rowTiles = (a0.B + 31) / 32;
+  float4 *quads = reinterpret_cast<float4 *>(smem);
 #pragma unroll
-  for (int e = 0; e < M; ++e) {
-    const LinearArgs &ae = a[e];
-    float *partial = split_partials(ae, false);
+  for (int e0 = 0; e0 < M; e0 += EM) {
+    if (e0 > 0) __syncthreads();
 #pragma unroll
-    for (int h = 0; h < J; h += JH) {
-      if (e > 0 || h > 0) __syncthreads();
+    for (int e = 0; e < EM && e0 + e < M; ++e)
 #pragma unroll
-      for (int j = 0; j < JH; ++j)
+      for (int j = 0; j < J; ++j)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) smem[((wave * JH + j) * 16 + r) * 64 + lane] = acc[e][h + j][r];
-      __syncthreads();
+        for (int rb = 0; rb < 4; ++rb)
+          quads[(((wave * EM + e) * J + j) * 4 + rb) * 64 + lane] = make_float4(
+              acc[e0 + e][j][4 * rb], acc[e0 + e][j][4 * rb + 1], acc[e0 + e][j][4 * rb + 2], acc[e0 + e][j][4 * rb + 3]);
+    __syncthreads();
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        float sum[JH];
+    for (int e = 0; e < EM && e0 + e < M; ++e) {
+      const LinearArgs &ae = a[e0 + e];
+      float *partial = split_partials(ae, false);
+      float sum[J][4];
 #pragma unroll
-        for (int j = 0; j < JH; ++j) sum[j] = smem[(j * 16 + 4 * wave + q) * 64 + lane];
+      for (int j = 0; j < J; ++j) {
+        const float4 t = quads[((e * J + j) * 4 + wave) * 64 + lane];
+        sum[j][0] = t.x; sum[j][1] = t.y; sum[j][2] = t.z; sum[j][3] = t.w;
 #pragma unroll
-        for (int v = 1; v < 4; ++v)
-#pragma unroll
-          for (int j = 0; j < JH; ++j) sum[j] += smem[((v * JH + j) * 16 + 4 * wave + q) * 64 + lane];
-        const int i = rt * 32 + 8 * wave + 4 * s + q;   // row of accumulator register 4*wave + q
-        if (!colOk) continue;
-        if (ae.kSplit > 1) {
-          float *p = partial + long(kg) * rowTiles * 32 * O + long(i) * O + n + h;
-          if (ae.deferred) {
-            if constexpr (JH == 2) *reinterpret_cast<float2 *>(p) = make_float2(sum[0], sum[1]);
-            else *p = sum[0];
-          } else {
-#pragma unroll
-            for (int j = 0; j < JH; ++j) partial_store(p + j, sum[j]);
-          }
-        } else if (i < ae.B) {
-          float *p = ae.dst + long(i) * O + n + h;
-          if constexpr (JH == 2) *reinterpret_cast<float2 *>(p) = make_float2(sum[0], sum[1]);
-          else *p = sum[0];
+        for (int v = 1; v < 4; ++v) {
+          const float4 o = quads[(((v * EM + e) * J + j) * 4 + wave) * 64 + lane];
+          sum[j][0] += o.x; sum[j][1] += o.y; sum[j][2] += o.z; sum[j][3] += o.w;
         }
       }
-    }
-    if (ae.kSplit > 1 && !ae.deferred) {
-      unsigned *counters = split_counters(ae);
-      if (split_arrive(counters + rt * ae.tilesN + tn, ae.kSplit))
-        split_finish(ae, partial, long(rowTiles) * 32 * O, rt * 32, 32, tn * 32 * J, 32 * J);
+      if (colOk) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int i = rt * 32 + 8 * wave + 4 * s + q;   // row of accumulator register 4*wave + q
+          float v[J];
+#pragma unroll
+          for (int j = 0; j < J; ++j) v[j] = sum[j][q];
+          if (ae.kSplit > 1) {
+            float *p = partial + long(kg) * rowTiles * 32 * O + long(i) * O + n;
+            if (ae.deferred) {
+              store_columns<J>(p, v);
+            } else {
+#pragma unroll
+              for (int j = 0; j < J; ++j) partial_store(p + j, v[j]);
+            }
+          } else if (i < ae.B) {
+            store_columns<J>(ae.dst + long(i) * O + n, v);
+          }
+        }
+      }
+      if (ae.kSplit > 1 && !ae.deferred) {
+        unsigned *counters = split_counters(ae);
+        if (split_arrive(counters + rt * ae.tilesN + tn, ae.kSplit))
+          split_finish(ae, partial, long(rowTiles) * 32 * O, rt * 32, 32, tn * 32 * J, 32 * J);
+      }
     }
   }
 }
@@ -867,7 +885,7 @@ template <bool NT> __device__ void linear_rowvec_stream(const LinearArgs &a, int
 }
 
 template <int J, int S, bool NT = false> __device__ void linear_mfma_body(const LinearArgs &a, int block) {
-  extern __shared__ float smem[];
+  extern __shared__ __attribute__((aligned(16))) float smem[];
   linear_mfma<J, S, 1, NT>(&a, block, smem);
 }
 CKL_ENTRY_ATTR(linear_rowvec, LinearArgs, linear_rowvec_stream<false>, 1024, )
@@ -891,12 +909,12 @@ CKL_ENTRY_ATTR(linear_mfma4x2, LinearArgs, (linear_mfma_body<4, 2>), kBlock, CKL
 #define CKL_LINEAR_SHARED(J, M)                                                                       \
   extern "C" __global__ __launch_bounds__(kBlock) CKL_ONE_WAVE void ckl_linear_mfma##J##x1_shared##M( \
       const Group<LinearArgs> g) {                                                                    \
-    extern __shared__ float smem[];                                                                   \
+    extern __shared__ __attribute__((aligned(16))) float smem[];                                                                   \
     linear_mfma<J, 1, M, false>(g.m, blockIdx.x, smem);                             \
   }                                                                                                   \
   extern "C" __global__ __launch_bounds__(kBlock) CKL_ONE_WAVE void ckl_linear_mfma##J##x1_nt_shared##M( \
       const Group<LinearArgs> g) {                                                                    \
-    extern __shared__ float smem[];                                                                   \
+    extern __shared__ __attribute__((aligned(16))) float smem[];                                                                   \
     linear_mfma<J, 1, M, true>(g.m, blockIdx.x, smem);                              \
   }
 CKL_LINEAR_SHARED(1, 2)

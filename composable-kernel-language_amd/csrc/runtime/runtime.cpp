@@ -1,5 +1,6 @@
 #include "runtime.h"
 #include "scratch.h"
+#include "../kernels/args.h"
 
 #include <algorithm>
 #include <chrono>
@@ -264,6 +265,11 @@ Launch groupLaunch(const std::vector<const Launch *> &members, bool shared) {
   blob.resize((blob.size() + 7) & ~size_t(7), 0);
   out.arguments = std::move(blob);
   out.grid[0] = shared ? first.grid[0] : unsigned(start);
+  // A shared-operand linear passes the accumulators of up to kLinearEpilogueBytes worth of members
+  // through LDS at once (linearEpilogueMembers, csrc/kernels/args.h); a member alone needs
+  // `first.shared` bytes.
+  if (shared && first.shared)
+    out.shared = unsigned(std::min<size_t>(members.size(), std::max<size_t>(1, ckl::kernels::kLinearEpilogueBytes / first.shared)) * first.shared);
   return out;
 }
 

@@ -103,6 +103,7 @@ def _rms_apply(shapes, consts, ext):
 # 16.1-16.4 us with J = 2, while a single projection of the same shape is slower with J = 1
 # (6.5 us against 7.2 us) and the gate/up pair is no faster with J = 2 (24.2 against 24.4 us).
 LINEAR_TARGET_GROUPS = 256    # MI355X compute units
+LINEAR_EPILOGUE_COLUMN_BYTES = 4 * 16 * 64 * 4   # LDS per weight column of a lane (4 waves x 16 registers)
 LINEAR_MIN_FILL = 0.85
 LINEAR_MIN_CHUNK = 256
 LINEAR_ZERO_PAGE = 256    # kZeroPage: leading workspace bytes that stay zero
@@ -134,7 +135,7 @@ def linear_tiling(b: int, i: int, o: int, members: int = 1) -> dict:
                 break
         _, j, tiles, split, chunk = best
         rows = row_tiles * 32
-        shared = 4 * min(j, 2) * 16 * 64 * 4          # the 4 waves' accumulator tiles, 2 columns at a time
+        shared = j * LINEAR_EPILOGUE_COLUMN_BYTES      # the 4 waves' accumulator tiles, one pass
         entry = f"ckl_linear_mfma{j}x1"
         block = BLOCK
     elif b <= LINEAR_VECTOR_ROWS:
