@@ -2,14 +2,18 @@
 """Decode-step benchmark of the CKL MI355X backend (one GPU).
 
 For each decoder configuration (small, wide, deep, large) the decode program is
-lowered, compiled with storage reuse off and on, bound to device-resident synthetic state,
-prefilled on the GPU (teacher-forced prompt), and timed per variant with the protocol of the
-reference harness (benchmarks/decoder/run.py:160-197): every sample resets the mutable state and
-times one 16-step generation (the configuration's greedy steps, capacity T = context + 16) with
-HIP events on the invocation stream; samples rotate and reverse the variant order; the median
-microseconds per decode step is reported.
+lowered, compiled with storage reuse off and on, bound to device-resident synthetic state and
+prefilled on the GPU (teacher-forced prompt). The NumPy checker (oracle/decoder.py, in a CPU-only
+child process) then computes the expected state after 1, 16 and any partial generation's steps
+from that prefilled state, and every variant is timed with the protocol of the reference harness
+(benchmarks/decoder/run.py:160-197): every sample resets the mutable state and times one
+generation with HIP events on the invocation stream; samples rotate and reverse the variant
+order; the median microseconds per decode step is reported. Every run is verified
+(run.py:172-196): each variant's first generation in full (tokens, history, position, logits,
+the cache rows written, the prefill rows and unused suffix unchanged, sentinel tails), every
+warmup and timed sample's tokens, history, position and logits, and the weights after all.
 
-Variants (run.py:24-38 plus two ablations):
+Variants (run.py:24-38 plus ablations):
   sequential / capture / inferred       ordinary launches, single-stream capture, inferred graph
   branches                              one graph node per dispatch with the reduced DAG's edges
                                         (the reference's inferred graph: branch concurrency only)
@@ -20,18 +24,22 @@ Variants (run.py:24-38 plus two ablations):
   *_reuse                               the same with storage reuse on
   batched_*                             16 steps per graph submission (storage reuse on)
 
---steps K is the number of decode steps timed per variant (ceil(K / 16) samples of one 16-step
-generation each); --warmup W the untimed warmup steps per variant. Neither changes the workload.
+--steps K: decode steps timed per variant, as generations of 16 steps from the prefilled state
+and one shorter generation for the remainder (a batched variant rounds its samples up to whole
+16-step submissions and reports its own count); --warmup W: untimed warmup steps per variant,
+likewise. Each variant's first (verified) generation precedes its warmup, as in run.py:170-178.
 
 Independent requests (`independent_requests`, small and wide): 8 invocations of one compiled
 program with shared weights, each on its own stream, bursts of one 16-step generation per request
-run side by side (ckl.run_requests), against the batching control (one invocation of 8 x B rows).
+run side by side (ckl.run_requests), against the batching control (one invocation of 8 x B rows);
+every burst's state is checked against the requests run one after another.
 
-Output: one JSON line on stdout; progress on stderr. The headline `value` is the large decoder's
-inferred-graph median µs/step (the largest single-GPU configuration of BASELINE.json). The CPU
-baseline (the NumPy restatement of the reference decoder step, oracle/decoder.py) runs in two
-child processes started before any GPU call (all cores, then one thread) from the GPU-prefilled
-state, after the GPU timing; the all-cores run is also the checker of the GPU's tokens and logits.
+Output: one short JSON line on stdout (headline, roofline, CPU baseline, one summary per other
+configuration); the full result (every variant's samples, kernel families, setup costs, vector
+pipeline, independent requests) goes to --output (default gpurun_out/bench_detail.json); progress
+on stderr. The headline `value` is the large decoder's inferred-graph median µs/step (the largest
+single-GPU configuration of BASELINE.json). The CPU baseline times the same NumPy decoder step in
+two child processes started before any GPU call (all cores, then one thread) after the GPU timing.
 """
 from __future__ import annotations
 
@@ -58,6 +66,7 @@ HBM_PEAK = 8.0e12          # MI355X HBM3E bytes/s
 METRIC = "median µs/decode step: inferred hipGraph vs stream capture; scratch bytes"
 HEADLINE = "large"
 GENERATION = 16            # greedy steps per generation
+DEFAULT_DETAIL = ROOT / "gpurun_out" / "bench_detail.json"
 
 
 def log(*parts):
@@ -71,6 +80,17 @@ def variants(steps):
             ("sequential_reuse", True, "ordinary", 1), ("capture_reuse", True, "capture", 1),
             ("inferred_reuse", True, "graph", 1), ("batched_capture", True, "capture", steps),
             ("batched_inferred", True, "graph", steps), ("batched_branches", True, "branches", steps)]
+
+
+def generations(total: int) -> list:
+    """Step counts of the generations that make up `total` decode steps: whole generations of
+    GENERATION steps, then the remainder."""
+    return [GENERATION] * (total // GENERATION) + ([total % GENERATION] if total % GENERATION else [])
+
+
+def submissions(count: int, group: int) -> int:
+    """Submissions of `group` steps that cover a generation of `count` steps."""
+    return max(1, math.ceil(count / group))
 
 
 def algorithmic_step_bytes(c, position):
@@ -109,25 +129,40 @@ def decoder_node_bytes(c, position):
     return nodes
 
 
+
+
 LIGHT_RESET = ("tokens", "position", "history", "logits")
 
 
-def time_variants(session, c, samples, warmup, log_prefix, only=None):
-    """Timing resets restore the small mutable state only: every run rewrites the cache rows it
-    reads (positions >= the prefill position) before reading them, with deterministic kernels."""
+def time_variants(session, c, steps, warmup, expected, log_prefix, only=None):
+    """Times every variant over `steps` decode steps (generations(steps)) after `warmup` untimed
+    ones, verifying every run against `expected` (step count -> expected state). Timing resets
+    restore the small mutable state only: every run rewrites the cache rows it reads (positions
+    >= the prefill position) before reading them, with deterministic kernels."""
     state = session.state
     rows = [row for row in variants(c.steps) if not only or row[0] in only]
     metrics = {name: [] for name, *_ in rows}
-    setup = {}
+    walls = {name: [] for name, *_ in rows}
+    timed = {name: 0 for name, *_ in rows}
+    setup, errors, checked = {}, {name: {} for name, *_ in rows}, {name: 0 for name, *_ in rows}
+
+    def verify(name, count, full=False):
+        found = state.verify_generation(expected[count], full=full, longest=c.steps)
+        for key, value in found.items():
+            errors[name][key] = max(errors[name].get(key, 0.0), value)
+        checked[name] += 1
+
     for name, reuse, mode, group in rows:
         inv = session.invocations[reuse]
         state.reset(LIGHT_RESET)
         setup[name] = inv.benchmark(iterations=1, mode=mode, batch_size=group)["graph_setup_ms"]
-        for _ in range(warmup):
+        verify(name, group, full=True)
+        for count in generations(warmup):
             state.reset(LIGHT_RESET)
-            inv.benchmark(iterations=c.steps // group, mode=mode, batch_size=group)
-    results = {}
-    for sample in range(samples):
+            k = submissions(count, group)
+            inv.benchmark(iterations=k, mode=mode, batch_size=group)
+            verify(name, k * group)
+    for sample, count in enumerate(generations(steps)):
         offset = sample % len(rows)
         order = rows[offset:] + rows[:offset]
         if sample % 2:
@@ -135,24 +170,34 @@ def time_variants(session, c, samples, warmup, log_prefix, only=None):
         for name, reuse, mode, group in order:
             inv = session.invocations[reuse]
             state.reset(LIGHT_RESET)
-            timing = inv.benchmark(iterations=c.steps // group, mode=mode, batch_size=group)
+            k = submissions(count, group)
+            timing = inv.benchmark(iterations=k, mode=mode, batch_size=group)
             metrics[name].append(timing["stream_us"])
-            results.setdefault(name, []).append(timing["wall_us"])
+            walls[name].append(timing["wall_us"])
+            timed[name] += k * group
+            verify(name, k * group)
+    state.verify_read_only()
     table = {}
     for name, reuse, mode, group in rows:
         inv = session.invocations[reuse]
         launches = inv.launch_count(mode=mode, batch_size=group)
         edges = inv.edge_count(mode=mode, batch_size=group)
         table[name] = dict(median_us=statistics.median(metrics[name]), min_us=min(metrics[name]),
-                           max_us=max(metrics[name]), wall_us=statistics.median(results[name]),
+                           max_us=max(metrics[name]), wall_us=statistics.median(walls[name]),
                            graph_setup_ms=setup[name], launches_per_submission=launches, graph_edges=edges,
-                           steps_per_submission=group, samples=metrics[name])
+                           steps_per_submission=group, timed_steps=timed[name], samples=metrics[name],
+                           runs_verified=checked[name], errors=errors[name])
         log(f"{log_prefix} {name:18s} {table[name]['median_us']:9.2f} us/step  launches/submission={launches}"
-            f" edges={edges}")
+            f" edges={edges} timed_steps={timed[name]} verified_runs={checked[name]}")
     return table
 
 
-def run_config(name, c, args, device):
+def heap_bytes(program) -> int:
+    return sum(int(line.split("bytes = ")[1].split(" ")[0]) for line in program.executable_ir.splitlines()
+               if '"ckl_exec.heap"' in line)
+
+
+def run_config(name, c, args, device, checker):
     from programs.harness import DecoderSession, synthetic_inputs
     t0 = time.time()
     arrays, prompts = synthetic_inputs(c, args.seed, init="baseline")
@@ -161,15 +206,11 @@ def run_config(name, c, args, device):
     session.prefill(prompts, mode="ordinary", progress=lambda done, total: log(f"[{name}] prefill {done}/{total}"))
     t2 = time.time()
     log(f"[{name}] inputs+compile+bind {t1 - t0:.1f}s, device prefill of {c.context - 1} steps {t2 - t1:.2f}s")
-    table = time_variants(session, c, args.samples, args.warmup_generations, f"[{name}]", args.variants)
-    heap = {}
-    for reuse, program in session.programs.items():
-        heap[str(reuse)] = sum(int(line.split("bytes = ")[1].split(" ")[0]) for line in program.executable_ir.splitlines()
-                               if '"ckl_exec.heap"' in line)
-    # State after one 16-step generation from the prefilled state (the CPU checker compares it).
-    session.state.reset()
-    session.invocations[True].run(mode="graph", batch_size=c.steps)
-    final = {k: session.state.download(k) for k in ("tokens", "history", "position", "logits")}
+    counts = {1, c.steps} | {n for n in generations(args.steps) + generations(args.warmup)}
+    expected = checker.expected(name, session, sorted(counts))
+    log(f"[{name}] expected states for {sorted(counts)} steps from the NumPy checker in {time.time() - t2:.1f}s")
+    table = time_variants(session, c, args.steps, args.warmup, expected, f"[{name}]", args.variants)
+    heap = {str(reuse): heap_bytes(program) for reuse, program in session.programs.items()}
 
     def median(variant):
         return table[variant]["median_us"] if variant in table else None
@@ -180,26 +221,34 @@ def run_config(name, c, args, device):
     position = c.context - 1
     mean_bytes = statistics.mean(algorithmic_step_bytes(c, position + s) for s in range(c.steps))
     step_us = median("inferred") or min(v["median_us"] for v in table.values())
+    normwise = max((v["errors"].get("logits_normwise", 0.0) for v in table.values()), default=None)
     result = dict(config=vars(c), steps=c.steps, variants=table,
                   inferred_us=median("inferred"), capture_us=median("capture"), ordinary_us=median("sequential"),
                   branches_us=median("branches"), contracted_us=median("contracted"),
+                  stream_us=median("inferred_stream"), inferred_reuse_us=median("inferred_reuse"),
                   batched_inferred_us=median("batched_inferred"),
                   inferred_over_capture=ratio("capture", "inferred"),
                   branches_over_capture=ratio("capture", "branches"),
                   contracted_over_capture=ratio("capture", "contracted"),
+                  stream_over_capture=ratio("capture", "inferred_stream"),
                   inferred_over_contracted=ratio("contracted", "inferred"),
                   inferred_reuse_over_capture_reuse=ratio("capture_reuse", "inferred_reuse"),
                   batched_branches_over_batched_capture=ratio("batched_capture", "batched_branches"),
                   scratch_bytes={"reuse_off": heap["False"], "reuse_on": heap["True"]},
+                  workspace_bytes={"reuse_off": session.invocations[False].workspace_bytes,
+                                   "reuse_on": session.invocations[True].workspace_bytes},
                   tokens_per_s=c.batch * 1e6 / step_us,
                   algorithmic_bytes_per_step=mean_bytes,
                   step_hbm_fraction=mean_bytes / (step_us * 1e-6) / HBM_PEAK,
+                  logits_normwise=normwise,
+                  runs_verified=sum(v["runs_verified"] for v in table.values()),
                   host_planning_ms={"lower": session.lower_ms, "compile_reuse_off": session.compile_ms[False],
                                     "compile_reuse_on": session.compile_ms[True]})
     log(f"[{name}] inferred/capture {result['inferred_over_capture']}; branches/capture {result['branches_over_capture']}; "
         f"contracted/capture {result['contracted_over_capture']}; scratch {heap['False']} -> {heap['True']} B; "
-        f"step roofline {result['step_hbm_fraction']:.3f} of 8 TB/s")
-    return session, result, final
+        f"workspaces {result['workspace_bytes']} B; step roofline {result['step_hbm_fraction']:.3f} of 8 TB/s; "
+        f"{result['runs_verified']} runs verified, logits normwise <= {normwise:.2e}")
+    return session, result
 
 
 def c_name(c):
@@ -294,7 +343,9 @@ def kernel_roofline(session, c, samples=7):
     return summary, dominant, roofline
 
 
-# ---------------------------------------------------------------------------- CPU baseline
+
+
+# ---------------------------------------------------------------------------- CPU side
 def cpu_threads() -> int:
     """Cores of this process's share: OMP_NUM_THREADS when set (16 on a one-GPU box), else the
     CPUs it may run on."""
@@ -321,11 +372,15 @@ def cpu_description() -> dict:
             "affinity_cpus": len(os.sched_getaffinity(0)), "numpy": np.__version__, "blas": blas}
 
 
-def start_cpu_workers(directory: Path):
-    """Start the two CPU-baseline processes now, before this process makes any GPU call: one with
-    BLAS/OpenMP threads = this process's cores, one with 1 thread. They wait for the states."""
+
+def start_cpu_workers(directory: Path, timing: bool):
+    """Start the CPU processes now, before this process makes any GPU call (their BLAS threads and
+    memory are then not shared with the GPU process): the checker, with BLAS/OpenMP threads = this
+    process's cores, which computes expected states on request and, with `timing`, then times the
+    decoder step; and with `timing` a 1-thread process that times it single-threaded."""
     workers = {}
-    for role, threads in (("all", cpu_threads()), ("single", 1)):
+    roles = (("all", cpu_threads()), ("single", 1)) if timing else (("all", cpu_threads()),)
+    for role, threads in roles:
         env = dict(os.environ, OMP_NUM_THREADS=str(threads), OPENBLAS_NUM_THREADS=str(threads),
                    MKL_NUM_THREADS=str(threads), BLIS_NUM_THREADS=str(threads))
         workers[role] = (threads, subprocess.Popen([sys.executable, str(Path(__file__).resolve()), "--cpu-worker",
@@ -341,90 +396,144 @@ def wait_for(path: Path, alive, limit_s: float) -> bool:
             return True
         if not alive():
             return path.exists()
-        time.sleep(0.2)
+        time.sleep(0.1)
     return False
 
 
+def load_state(folder: Path, mutable) -> dict:
+    """The saved prefilled state: weights read-only, mutable arrays as copy-on-write views."""
+    return {p.stem: np.load(p, mmap_mode="c" if p.stem in mutable else "r") for p in folder.glob("*.npy")}
+
+
+def check_request(directory: Path, request: Path) -> None:
+    """Expected states of one configuration: oracle.decoder.step from the saved prefilled state,
+    the tokens, history, position, logits and written cache rows kept after each requested count."""
+    from oracle import decoder as oracle
+    from programs.decoder_config import Config
+    spec = json.loads(request.read_text())
+    c = Config(**spec["shape"])
+    state = load_state(directory / spec["name"], oracle.MUTABLE)
+    start = int(state["position"][0])
+    counts = sorted(spec["counts"])
+    out = {}
+    for n in range(1, counts[-1] + 1):
+        oracle.step(state, c)
+        if n in counts:
+            for key in ("tokens", "history", "position", "logits"):
+                out[f"{n}.{key}"] = np.array(state[key])
+            for key in ("kc", "vc"):
+                out[f"{n}.{key}_rows"] = np.array(state[key][:, :, :, start:start + n])
+    partial = directory / f"check.{spec['name']}.tmp.npz"
+    np.savez(partial, **out)
+    partial.rename(directory / f"check.{spec['name']}.npz")
+
+
 def cpu_worker(directory: Path, role: str) -> None:
-    """Times oracle.decoder.step (the NumPy restatement of the reference's decode step) on the
-    prefilled states the benchmark leaves in `directory`; the "all" role also records the state
-    after one 16-step generation for the benchmark to check the GPU's against."""
+    """The CPU side of the benchmark. The "all" role answers check requests (check.<config>.json)
+    as they come, then, on `go`, times oracle.decoder.step (the NumPy restatement of the
+    reference's decode step) on each saved prefilled state; the "single" role waits for
+    `go_single`. Either ends on `stop` or when the benchmark process is gone."""
     from oracle import decoder as oracle
     from programs.decoder_config import Config
     parent = os.getppid()
     go = directory / ("go" if role == "all" else "go_single")
-    if not wait_for(go, lambda: os.getppid() == parent, 3 * 3600):
-        return
+    answered = set()
+    deadline = time.time() + 3 * 3600
+    while True:
+        if os.getppid() != parent or (directory / "stop").exists() or time.time() > deadline:
+            return
+        if role == "all":
+            for request in sorted(directory.glob("check.*.json")):
+                if request.name not in answered:
+                    check_request(directory, request)
+                    answered.add(request.name)
+        if go.exists():
+            break
+        time.sleep(0.05)
     manifest = json.loads(go.read_text())
     for name in manifest["configs"]:
         plan = manifest["plan"][name][role]
         c = Config(**manifest["shapes"][name])
-        folder = directory / name
-        weights = {p.stem: np.load(p, mmap_mode="r") for p in folder.glob("*.npy") if p.stem not in oracle.MUTABLE}
         times = []
         for sample in range(plan["samples"]):
-            # Copy-on-write views: each sample starts from the prefilled state without copying it.
-            state = dict(weights, **{k: np.load(folder / f"{k}.npy", mmap_mode="c") for k in oracle.MUTABLE})
+            state = load_state(directory / name, oracle.MUTABLE)     # each sample from the prefilled state
             start = time.perf_counter()
             for _ in range(plan["steps"]):
                 oracle.step(state, c)
             times.append((time.perf_counter() - start) / plan["steps"] * 1e6)
-            if role == "all" and sample == 0:
-                np.savez(directory / f"{name}.check.npz", **{k: np.asarray(state[k]) for k in
-                                                              ("tokens", "history", "position", "logits")})
         (directory / f"{name}.{role}.json").write_text(json.dumps(
             {"us_per_step": statistics.median(times), "samples": plan["samples"], "steps": plan["steps"], "times": times}))
     (directory / f"done.{role}").write_text("ok")
 
 
-def save_state(directory: Path, name: str, session) -> None:
-    folder = directory / name
-    folder.mkdir(parents=True, exist_ok=True)
-    for key, value in session.state.initial.items():
-        np.save(folder / f"{key}.npy", np.ascontiguousarray(value))
+class Checker:
+    """Expected decoder states from the CPU checker process (oracle/decoder.py run on the
+    GPU-prefilled state), and the CPU baseline timing at the end."""
 
+    def __init__(self, directory: Path, workers: dict):
+        self.directory, self.workers = directory, workers
 
-def cpu_baselines(directory: Path, workers, configs: dict, finals: dict) -> dict:
-    """Release the workers (all cores, then one thread), collect timings and check the GPU's final
-    tokens, history, position and logits against the all-cores run's."""
-    from programs.decoder_config import CONFIGS
-    from programs.harness import LOGITS_NORMWISE, normwise_error
-    names = [n for n in configs if (directory / n).exists()]
-    plan = {n: {"all": {"samples": 1 if n == "large" else 7, "steps": GENERATION},
-                "single": {"samples": 1 if n == "large" else 3, "steps": 4 if n == "large" else GENERATION}}
-            for n in names}
-    manifest = json.dumps({"configs": names, "plan": plan, "shapes": {n: vars(CONFIGS[n]) for n in names}})
-    out = {}
-    (directory / "go").write_text(manifest)
-    ok = wait_for(directory / "done.all", lambda: workers["all"][1].poll() is None, 3600)
-    (directory / "go_single").write_text(manifest)
-    ok_single = wait_for(directory / "done.single", lambda: workers["single"][1].poll() is None, 3600)
-    for role, (threads, process) in workers.items():
-        try:
-            process.wait(timeout=60)
-        except subprocess.TimeoutExpired:
-            process.kill()
-    if not ok:
-        log("[cpu] the all-cores CPU baseline did not finish")
+    def alive(self, role="all") -> bool:
+        return self.workers[role][1].poll() is None
+
+    def expected(self, name: str, session, counts) -> dict:
+        folder = self.directory / name
+        folder.mkdir(parents=True, exist_ok=True)
+        for key, value in session.state.initial.items():
+            np.save(folder / f"{key}.npy", np.ascontiguousarray(value))
+        request = self.directory / f"check.{name}.json"
+        partial = self.directory / f"request.{name}.tmp"
+        partial.write_text(json.dumps({"name": name, "shape": vars(session.config), "counts": list(counts)}))
+        partial.rename(request)
+        answer = self.directory / f"check.{name}.npz"
+        if not wait_for(answer, self.alive, 1800):
+            raise RuntimeError(f"the NumPy checker gave no expected state for {name}")
+        with np.load(answer) as data:
+            out = {n: {"steps": n, **{key: data[f"{n}.{key}"] for key in
+                                      ("tokens", "history", "position", "logits", "kc_rows", "vc_rows")}}
+                   for n in counts}
+        answer.unlink()
         return out
-    for n in names:
-        row = json.loads((directory / f"{n}.all.json").read_text())
-        check = np.load(directory / f"{n}.check.npz")
-        final = finals[n]
-        tokens = bool(all(np.array_equal(final[k], check[k]) for k in ("tokens", "history", "position")))
-        normwise = normwise_error(final["logits"], check["logits"])
-        entry = {"value": row["us_per_step"], "unit": "us/step", "cores": workers["all"][0], "kind": "port",
-                 "sample": f"{row['samples']} x {row['steps']}-step NumPy generation(s) of oracle/decoder.py from the "
-                           f"GPU-prefilled state, B={CONFIGS[n].batch}",
-                 "tokens_match": tokens, "logits_normwise": normwise, "logits_normwise_ok": normwise <= LOGITS_NORMWISE,
-                 "logits_allclose": bool(np.allclose(final["logits"], check["logits"], atol=2e-5, rtol=3e-4))}
-        if ok_single and (directory / f"{n}.single.json").exists():
-            single = json.loads((directory / f"{n}.single.json").read_text())
-            entry["single_thread"] = {"value": single["us_per_step"], "unit": "us/step", "cores": 1,
-                                      "sample": f"{single['samples']} x {single['steps']}-step generation(s)"}
-        out[n] = entry
-        log(f"[cpu] {n}: {entry}")
-    return out
+
+    def baselines(self, configs: dict) -> dict:
+        """Release the timing processes (all cores, then one thread) and collect their timings."""
+        from programs.decoder_config import CONFIGS
+        if "single" not in self.workers:
+            (self.directory / "stop").write_text("")
+            return {}
+        names = [n for n in configs if (self.directory / n).exists()]
+        plan = {n: {"all": {"samples": 1 if n == "large" else 7, "steps": GENERATION},
+                    "single": {"samples": 1 if n == "large" else 3, "steps": 4 if n == "large" else GENERATION}}
+                for n in names}
+        manifest = json.dumps({"configs": names, "plan": plan, "shapes": {n: vars(CONFIGS[n]) for n in names}})
+        out = {}
+        (self.directory / "go").write_text(manifest)
+        ok = wait_for(self.directory / "done.all", self.alive, 3600)
+        (self.directory / "go_single").write_text(manifest)
+        ok_single = wait_for(self.directory / "done.single", lambda: self.alive("single"), 3600)
+        if not ok:
+            log("[cpu] the all-cores CPU baseline did not finish")
+            return out
+        for n in names:
+            row = json.loads((self.directory / f"{n}.all.json").read_text())
+            entry = {"value": row["us_per_step"], "unit": "us/step", "cores": self.workers["all"][0], "kind": "port",
+                     "sample": f"{row['samples']} x {row['steps']}-step NumPy generation(s) of oracle/decoder.py "
+                               f"from the GPU-prefilled state, B={CONFIGS[n].batch}"}
+            if ok_single and (self.directory / f"{n}.single.json").exists():
+                single = json.loads((self.directory / f"{n}.single.json").read_text())
+                entry["single_thread"] = {"value": single["us_per_step"], "unit": "us/step", "cores": 1,
+                                          "sample": f"{single['samples']} x {single['steps']}-step generation(s)"}
+            out[n] = entry
+            log(f"[cpu] {n}: {entry}")
+        return out
+
+    def close(self):
+        (self.directory / "stop").write_text("")
+        for _, process in self.workers.values():
+            try:
+                process.wait(timeout=30)
+            except subprocess.TimeoutExpired:
+                process.kill()
 
 
 # ---------------------------------------------------------------------------- setup cost
@@ -468,13 +577,30 @@ REQUEST_RUNS = (("serial_inferred", "graph", 1, True), ("ordinary", "ordinary", 
                 ("inferred_group16", "graph", GENERATION, False), ("inferred_stream", "stream", 1, False))
 
 
+def request_states(group) -> list:
+    return [{k: state.download(k) for k in ("tokens", "history", "position", "logits")} for state in group.states]
+
+
+def check_requests(group, reference: list, label: str) -> None:
+    """Every request's state after a burst equals its state after the same burst run one request
+    after another: tokens, history and position exactly, logits within the row-normwise bound."""
+    from programs.harness import LOGITS_NORMWISE, normwise_error
+    for index, (got, want) in enumerate(zip(request_states(group), reference)):
+        for key in ("tokens", "history", "position"):
+            if not np.array_equal(got[key], want[key]):
+                raise AssertionError(f"requests {label}: request {index} {key} differs from the serial run")
+        if normwise_error(got["logits"], want["logits"]) > LOGITS_NORMWISE:
+            raise AssertionError(f"requests {label}: request {index} logits differ from the serial run")
+
+
 def independent_requests(device, names, samples):
     """Independent requests (benchmarks/decoder/experiment.py:20-147; REPORT.md "Independent
     requests and the batching control"): REQUESTS invocations of one compiled decode program with
     shared weights and distinct prompts, GPU-prefilled, each timed 16-step generation burst run
     side by side on their own streams (or one after another: serial_inferred); and the batching
     control, one invocation of the same model with REQUESTS x B rows. Median burst wall and GPU
-    span over `samples` rotated/reversed bursts, tokens/s = requests x B x 16 / wall."""
+    span over `samples` rotated/reversed bursts, tokens/s = requests x B x 16 / wall. Every burst
+    is checked against the first serial burst."""
     from programs.decoder_config import CONFIGS, Config
     from programs.harness import DecoderSession, RequestGroup, synthetic_inputs
     out = {}
@@ -484,9 +610,15 @@ def independent_requests(device, names, samples):
         group = RequestGroup(c, device, [arrays for arrays, _ in inputs])
         group.prefill([prompts for _, prompts in inputs])
         rows = {label: {"wall_us": [], "span_us": []} for label, *_ in REQUEST_RUNS}
+        reference = None
+        checked = 0
         for label, mode, batch, serial in REQUEST_RUNS:          # warm: graphs built, clocks up
             group.reset()
             group.run(mode=mode, iterations=GENERATION // batch, batch_size=batch, serial=serial)
+            if reference is None:
+                reference = request_states(group)
+            check_requests(group, reference, label)
+            checked += 1
         for sample in range(samples):
             order = list(REQUEST_RUNS[sample % len(REQUEST_RUNS):] + REQUEST_RUNS[:sample % len(REQUEST_RUNS)])
             for label, mode, batch, serial in (order if sample % 2 == 0 else reversed(order)):
@@ -494,6 +626,8 @@ def independent_requests(device, names, samples):
                 t = group.run(mode=mode, iterations=GENERATION // batch, batch_size=batch, serial=serial)
                 rows[label]["wall_us"].append(t["wall_us"])
                 rows[label]["span_us"].append(t["span_us"])
+                check_requests(group, reference, label)
+                checked += 1
         tokens = REQUESTS * c.batch * GENERATION
         result = {label: {"wall_ms": statistics.median(r["wall_us"]) / 1e3, "span_ms": statistics.median(r["span_us"]) / 1e3,
                           "tokens_per_s": tokens / (statistics.median(r["wall_us"]) * 1e-6)}
@@ -506,6 +640,7 @@ def independent_requests(device, names, samples):
         session = DecoderSession(wide, device, arrays=arrays)
         session.prefill(prompts)
         control = {}
+        control_reference = None
         for label, batch in (("batched_inferred", 1), ("batched_inferred_group16", GENERATION)):
             inv = session.invocations[True]
             session.state.reset()
@@ -514,15 +649,20 @@ def independent_requests(device, names, samples):
             for _ in range(samples):
                 session.state.reset()
                 runs.append(inv.benchmark(iterations=GENERATION // batch, mode="graph", batch_size=batch))
+                got = {k: session.state.download(k) for k in ("tokens", "history", "position", "logits")}
+                control_reference = control_reference or got
+                if not all(np.array_equal(got[k], control_reference[k]) for k in got):
+                    raise AssertionError(f"batching control {label}: runs differ")
+                checked += 1
             wall = statistics.median(r["wall_us"] for r in runs) * GENERATION
             control[label] = {"wall_ms": wall / 1e3,
                               "span_ms": statistics.median(r["stream_us"] for r in runs) * GENERATION / 1e3,
                               "tokens_per_s": tokens / (wall * 1e-6)}
         del session
         out[name] = {"requests": REQUESTS, "rows_per_request": c.batch, "steps": GENERATION,
-                     "independent": result, "batching_control": control}
+                     "independent": result, "batching_control": control, "bursts_verified": checked}
         log(f"[requests] {name}: " + "; ".join(f"{k} {v['wall_ms']:.3f} ms {v['tokens_per_s']:.0f} tok/s"
-                                               for k, v in {**result, **control}.items()))
+                                               for k, v in {**result, **control}.items()) + f"; {checked} verified")
     return out
 
 
@@ -564,18 +704,33 @@ def vector_pipeline(device, samples):
     return out
 
 
+
+def summary_line(name, r):
+    """The few figures of a non-headline configuration that the stdout line carries."""
+    keep = ("inferred_us", "capture_us", "branches_us", "contracted_us", "stream_us", "ordinary_us",
+            "inferred_reuse_us", "inferred_over_capture", "branches_over_capture", "scratch_bytes", "workspace_bytes",
+            "step_hbm_fraction", "logits_normwise", "runs_verified")
+    out = {k: r[k] for k in keep}
+    if "cpu_baseline" in r:
+        out["cpu_us"] = r["cpu_baseline"]["value"]
+    return out
+
+
 def main():
     parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=7 * GENERATION,
-                        help="decode steps timed per variant: ceil(steps / 16) samples of one 16-step generation")
+                        help="decode steps timed per variant (generations of 16 steps, then the remainder)")
     parser.add_argument("--warmup", type=int, default=3 * GENERATION, help="untimed warmup decode steps per variant")
     parser.add_argument("--seed", type=int, default=123)
     parser.add_argument("--configs", nargs="+", default=["small", "wide", "deep", "large"])
     parser.add_argument("--variants", nargs="+", default=None, choices=[v[0] for v in variants(GENERATION)],
                         help="time only these variants (default: all)")
-    parser.add_argument("--no-cpu-baseline", action="store_true")
-    parser.add_argument("--output", type=Path, default=None, help="also write the full JSON result here")
+    parser.add_argument("--no-cpu-baseline", action="store_true",
+                        help="skip the CPU timing (the NumPy checker still verifies every run)")
+    parser.add_argument("--no-extras", action="store_true",
+                        help="skip the setup-cost, vector-pipeline and independent-request measurements")
+    parser.add_argument("--output", type=Path, default=DEFAULT_DETAIL, help="where the full JSON result is written")
     parser.add_argument("--cpu-worker", type=Path, default=None, help=argparse.SUPPRESS)
     parser.add_argument("--role", default="all", help=argparse.SUPPRESS)
     args = parser.parse_args()
@@ -586,37 +741,31 @@ def main():
         print(json.dumps({"error": "this build measures one GPU: every box here has one MI355X, and the decode "
                           "step's sharding over requests or heads is a design note, not a measured path"}))
         sys.exit(2)
-    args.samples = max(1, math.ceil(args.steps / GENERATION))
-    args.warmup_generations = max(0, math.ceil(args.warmup / GENERATION))
+    if args.steps < 1 or args.warmup < 0:
+        parser.error("--steps must be positive and --warmup nonnegative")
 
-    workdir, workers = None, None
-    if not args.no_cpu_baseline:
-        shm = Path("/dev/shm")
-        base = shm if shm.is_dir() and shutil.disk_usage(shm).free > 24 << 30 else None
-        workdir = Path(tempfile.mkdtemp(prefix="ckl_cpu_baseline_", dir=base))
-        workers = start_cpu_workers(workdir)
+    shm = Path("/dev/shm")
+    base = shm if shm.is_dir() and shutil.disk_usage(shm).free > 24 << 30 else None
+    workdir = Path(tempfile.mkdtemp(prefix="ckl_bench_", dir=base))
+    checker = Checker(workdir, start_cpu_workers(workdir, timing=not args.no_cpu_baseline))
     try:
-        line = measure(args, workdir, workers)
+        line = measure(args, checker)
     finally:
-        if workers:
-            for _, process in workers.values():
-                if process.poll() is None:
-                    process.kill()
-        if workdir:
-            shutil.rmtree(workdir, ignore_errors=True)
-    print(json.dumps(line, default=float))
+        checker.close()
+        shutil.rmtree(workdir, ignore_errors=True)
+    print(json.dumps(line, default=float), flush=True)
 
 
-def measure(args, workdir, workers):
+def measure(args, checker):
     import ckl
     from programs.decoder_config import CONFIGS
 
     device = ckl.Device()
     log(f"device: {device.name}")
-    configs, finals = {}, {}
+    configs = {}
     for name in args.configs:
         c = CONFIGS[name]
-        session, result, final = run_config(name, c, args, device)
+        session, result = run_config(name, c, args, device, checker)
         summary, dominant, roofline = kernel_roofline(session, c)
         result["kernels"] = summary
         for family, row in summary.items():
@@ -630,19 +779,18 @@ def measure(args, workdir, workers):
                                      for k, v in summary.items()}
         result["roofline"] = roofline
         log(f"[{name}] dominant kernel {dominant}: {roofline}")
-        result["setup"] = setup_costs(session)
-        log(f"[{name}] setup: {result['setup']}")
-        configs[name], finals[name] = result, final
-        if workdir:
-            save_state(workdir, name, session)
+        if not args.no_extras:
+            result["setup"] = setup_costs(session)
+            log(f"[{name}] setup: {result['setup']}")
+        configs[name] = result
         del session
-    vector = vector_pipeline(device, 7)
-    requests = independent_requests(device, [n for n in ("small", "wide") if n in args.configs], 7)
-    cpu = cpu_baselines(workdir, workers, configs, finals) if workdir else {}
+    extras = {}
+    if not args.no_extras:
+        extras["vector_pipeline"] = vector_pipeline(device, 7)
+        extras["independent_requests"] = independent_requests(device, [n for n in ("small", "wide") if n in args.configs], 7)
+    cpu = checker.baselines(configs)
     for name, row in cpu.items():
         configs[name]["cpu_baseline"] = row
-        configs[name]["tokens_match_cpu"] = row["tokens_match"]
-        configs[name]["logits_normwise"] = row["logits_normwise"]
     headline = HEADLINE if HEADLINE in configs else list(configs)[-1]
     head = configs[headline]
     c = CONFIGS[headline]
@@ -650,37 +798,36 @@ def measure(args, workdir, workers):
     host = cpu_description()
     baseline = None
     if headline in cpu:
-        baseline = dict(cpu[headline], **host, planner_ms=head["host_planning_ms"])
-    timed = args.samples * c.steps
+        baseline = dict(cpu[headline], cpu_model=host["cpu_model"], blas=host["blas"],
+                        planner_ms=head["host_planning_ms"])
+    timed = head["variants"]["inferred"]["timed_steps"] if "inferred" in head["variants"] else args.steps
+    roofline = {k: head["roofline"][k] for k in ("bound", "kernel", "achieved", "peak", "unit", "frac", "traffic",
+                                                 "algorithmic_bytes_per_launch", "avg_launch_us", "launches_per_step")}
     line = {
         "metric": METRIC, "value": value, "unit": "us/step", "n_gpus": 1, "steps": timed,
-        "warmup": args.warmup_generations * c.steps, "ms_per_step": value / 1000.0, "higher_is_better": False,
+        "warmup": args.warmup, "ms_per_step": value / 1000.0, "higher_is_better": False,
         "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "data": "synthetic (seeded N(0,0.02) weights, 1+N(0,0.02) gains, random prompts; GPU teacher-forced prefill)",
         "config": {"workload": f"{headline} decoder (B{c.batch} C{c.hidden} A{c.heads}x{c.head_dim} L{c.layers} "
                                f"F{c.ffn} V{c.vocab}, {c.context}-token prompt -> T {c.capacity}, {c.steps} greedy steps)",
-                   "inferred_us": head["inferred_us"], "capture_us": head["capture_us"],
-                   "ordinary_us": head["ordinary_us"], "branches_us": head["branches_us"],
-                   "contracted_us": head["contracted_us"], "batched_inferred_us": head["batched_inferred_us"],
-                   "inferred_over_capture": head["inferred_over_capture"],
-                   "branches_over_capture": head["branches_over_capture"],
-                   "contracted_over_capture": head["contracted_over_capture"],
-                   "scratch_bytes": head["scratch_bytes"], "tokens_per_s": head["tokens_per_s"],
-                   "step_hbm_fraction": head["step_hbm_fraction"], "logits_normwise": head.get("logits_normwise")},
-        "roofline": head["roofline"],
+                   **{k: head[k] for k in ("inferred_us", "capture_us", "ordinary_us", "branches_us", "contracted_us",
+                                           "stream_us", "inferred_reuse_us", "batched_inferred_us",
+                                           "inferred_over_capture", "branches_over_capture",
+                                           "contracted_over_capture", "stream_over_capture", "scratch_bytes",
+                                           "workspace_bytes", "tokens_per_s", "step_hbm_fraction",
+                                           "logits_normwise", "runs_verified")},
+                   "verification": "every run of every variant against the NumPy decoder (oracle/decoder.py) from "
+                                   "the GPU-prefilled state: tokens, history, position exact; logits atol 2e-5 rtol "
+                                   "3e-4 and row-normwise <= 1e-4; first run per variant also cache rows, prefix, "
+                                   "suffix, tails; weights after all"},
+        "roofline": roofline,
         "cpu_baseline": baseline,
-        "configs": {k: {kk: vv for kk, vv in v.items() if kk not in ("variants", "kernels")} |
-                    {"variants": {vn: {"median_us": vv["median_us"], "launches": vv["launches_per_submission"],
-                                       "edges": vv["graph_edges"], "wall_us": vv["wall_us"],
-                                       "graph_setup_ms": vv["graph_setup_ms"]}
-                                  for vn, vv in v["variants"].items()}} for k, v in configs.items()},
-        "vector_pipeline": vector,
-        "independent_requests": requests,
-        "host": host,
+        "other_configs": {k: summary_line(k, v) for k, v in configs.items() if k != headline},
+        "detail": str(args.output),
     }
-    if args.output:
-        full = dict(line, configs_full=configs)
-        args.output.write_text(json.dumps(full, indent=1, default=float) + "\n")
+    args.output.parent.mkdir(parents=True, exist_ok=True)
+    full = dict(line, host=host, configs=configs, **extras)
+    args.output.write_text(json.dumps(full, indent=1, default=float) + "\n")
     return line
 
 

@@ -444,6 +444,15 @@ int ckl_invocation_graph_instantiations(ckl_invocation *invocation, uint64_t *co
   });
 }
 
+int ckl_invocation_memory(ckl_invocation *invocation, uint64_t out[3]) {
+  return guarded([&] {
+    require(invocation, "invocation");
+    require(out, "out");
+    const auto m = invocation->invocation->memory();
+    for (int k = 0; k < 3; ++k) out[k] = m[k];
+  });
+}
+
 uint64_t ckl_invocation_node_count(ckl_invocation *invocation) {
   return invocation ? invocation->invocation->nodeCount() : 0;
 }

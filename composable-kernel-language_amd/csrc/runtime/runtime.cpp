@@ -806,6 +806,14 @@ std::array<double, 3> Invocation::benchmark(int mode, uint64_t iterations, uint6
   return result;
 }
 
+std::array<uint64_t, 3> Invocation::memory() const {
+  std::array<uint64_t, 3> out{0, 0, allocations};
+  for (const auto &h : heaps)
+    if (h) out[0] += h->bytes;
+  for (const auto &w : workspaces) out[1] += w->bytes;
+  return out;
+}
+
 double Invocation::timeNode(size_t index, uint64_t iterations) {
   std::lock_guard<std::mutex> lock(runMutex);
   return timeLaunch(plan.nodes.at(index).launch, iterations);
@@ -987,6 +995,7 @@ extern "C" void ckl_heap(void *frame, uint64_t id, uint64_t bytes) {
     if (f.heaps.size() <= id) f.heaps.resize(id + 1);
     f.heaps[id] = f.staticArena ? ckl::rt::importBuffer(f.device, f.carve(bytes), bytes)
                                 : ckl::rt::allocateBuffer(f.device, bytes);
+    if (!f.staticArena) ++f.allocations;
   });
 }
 
@@ -1054,6 +1063,7 @@ extern "C" void ckl_workspace(void *frame, uint64_t bytes) {
       ckl::rt::staticScratchClear(buffer->address(), rounded, f.stream);
     } else {
       buffer = ckl::rt::allocateBuffer(f.device, bytes);
+      ++f.allocations;
       ckl::rt::check(hipMemset(reinterpret_cast<void *>(buffer->address()), 0, bytes), "hipMemset(workspace)");
       ckl::rt::check(hipDeviceSynchronize(), "hipDeviceSynchronize");
     }

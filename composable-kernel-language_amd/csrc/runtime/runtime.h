@@ -189,6 +189,7 @@ struct Invocation {
   const uint64_t *bindingAddresses = nullptr;
   size_t bindingCount = 0;
   uint64_t instantiations = 0;                      // graph executables built for this invocation
+  uint64_t allocations = 0;                         // device allocations the bind made
 
   Invocation(std::shared_ptr<ProgramState> program, std::shared_ptr<Device> device, hipStream_t external = nullptr);
   ~Invocation();
@@ -201,6 +202,8 @@ struct Invocation {
   // graphs and any graph whose units change are dropped and rebuilt at their next use.
   void rebind(const std::vector<Argument> &arguments);
   uint64_t graphInstantiations();
+  // {planned heap bytes, library workspace bytes, device allocations made by the bind}.
+  std::array<uint64_t, 3> memory() const;
   size_t nodeCount() const { return plan.nodes.size(); }
   size_t graphNodeCount(int mode, uint64_t batch);
   size_t graphEdgeCount(int mode, uint64_t batch);

@@ -158,6 +158,65 @@ class DecoderState:
                         raise AssertionError(f"{name}: unused cache suffix changed")
         return max(errors.values(), default=0.0)
 
+    def verify_generation(self, expected: dict, *, full: bool, longest: int) -> dict:
+        """Check the state after a generation of `expected["steps"]` steps from the reset point
+        (the checks of benchmarks/decoder/run.py:107-132 that a timed sample can fail): tokens,
+        history and position exact; logits finite, within atol 2e-5 / rtol 3e-4 and the
+        row-normwise LOGITS_NORMWISE; those buffers' sentinel tails intact. With `full`, also the
+        cache rows the generation wrote (same tolerance), the prefill rows before them and every
+        row past the longest generation (`longest` steps) unchanged, and the caches' tails.
+        `expected` holds tokens, history, position, logits and the written cache rows
+        (kc_rows, vc_rows: [L, B, A, steps, D]). Returns the largest errors."""
+        out = {}
+        for name in ("tokens", "history", "position", "logits"):
+            actual = self.download(name, with_tail=True)
+            size = self.initial[name].size
+            if not np.all(actual[size:] == SENTINEL):
+                raise AssertionError(f"{name}: tail overwritten")
+            actual = actual[:size].reshape(self.initial[name].shape)
+            if name != "logits":
+                if not np.array_equal(actual, expected[name]):
+                    raise AssertionError(f"{name}: mismatch after {expected['steps']} steps")
+                continue
+            if not np.all(np.isfinite(actual)) or not np.allclose(actual, expected[name], atol=2e-5, rtol=3e-4):
+                raise AssertionError(f"logits: numerical mismatch, max error {np.max(np.abs(actual - expected[name]))}")
+            out["logits_max_abs"] = float(np.max(np.abs(actual - expected[name])))
+            out["logits_normwise"] = normwise_error(actual, expected[name])
+            if out["logits_normwise"] > LOGITS_NORMWISE:
+                raise AssertionError(f"logits: row-normwise error {out['logits_normwise']:.3e} > {LOGITS_NORMWISE}")
+        if not full:
+            return out
+        start, steps = int(self.initial["position"][0]), int(expected["steps"])
+        for name in ("kc", "vc"):
+            actual = self.download(name, with_tail=True)
+            size = self.initial[name].size
+            if not np.all(actual[size:] == SENTINEL):
+                raise AssertionError(f"{name}: tail overwritten")
+            actual = actual[:size].reshape(self.initial[name].shape)
+            initial = self.initial[name]
+            for layer in range(actual.shape[0]):      # one layer at a time bounds the temporaries
+                if not np.array_equal(actual[layer, :, :, :start], initial[layer, :, :, :start]):
+                    raise AssertionError(f"{name}: prefilled cache changed (layer {layer})")
+                if not np.array_equal(actual[layer, :, :, start + longest:], initial[layer, :, :, start + longest:]):
+                    raise AssertionError(f"{name}: unused cache suffix changed (layer {layer})")
+            rows = actual[:, :, :, start:start + steps]
+            reference = expected[f"{name}_rows"]
+            if not np.all(np.isfinite(rows)) or not np.allclose(rows, reference, atol=2e-5, rtol=3e-4):
+                raise AssertionError(f"{name}: written rows differ, max error {np.max(np.abs(rows - reference))}")
+            out[f"{name}_max_abs"] = float(np.max(np.abs(rows - reference)))
+        return out
+
+    def verify_read_only(self) -> None:
+        """Weights, RoPE table and every sentinel tail unchanged (run.py:114-120)."""
+        for name in shapes(self.config):
+            actual = self.download(name, with_tail=True)
+            size = self.initial[name].size
+            if not np.all(actual[size:] == SENTINEL):
+                raise AssertionError(f"{name}: tail overwritten")
+            if name not in MUTABLE and not np.array_equal(actual[:size].reshape(self.initial[name].shape),
+                                                          self.initial[name]):
+                raise AssertionError(f"{name}: model weights/input metadata changed")
+
 
 class DecoderSession:
     """Lowered decode program compiled with storage reuse off and on, bound to one state."""

@@ -79,6 +79,7 @@ _SIGNATURES = {
     "ckl_profiler_region": ([ctypes.c_int], ctypes.c_int),
     "ckl_invocation_rebind": ([ctypes.c_void_p, ctypes.POINTER(Argument), ctypes.c_size_t], ctypes.c_int),
     "ckl_invocation_graph_instantiations": ([ctypes.c_void_p, ctypes.POINTER(ctypes.c_uint64)], ctypes.c_int),
+    "ckl_invocation_memory": ([ctypes.c_void_p, ctypes.POINTER(ctypes.c_uint64)], ctypes.c_int),
     "ckl_invocations_run": ([ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t, ctypes.c_int, ctypes.c_uint64,
                              ctypes.c_uint64, ctypes.c_int, ctypes.POINTER(ctypes.c_double)], ctypes.c_int),
     "ckl_invocation_launch_count": ([ctypes.c_void_p, ctypes.c_int, ctypes.c_uint64, ctypes.POINTER(ctypes.c_uint64)],

@@ -333,6 +333,26 @@ class Invocation(_Closable):
         self._call(_native.native().ckl_invocation_graph_instantiations, ctypes.byref(count))
         return int(count.value)
 
+    def _memory(self) -> list:
+        out = (ctypes.c_uint64 * 3)()
+        self._call(_native.native().ckl_invocation_memory, out)
+        return [int(v) for v in out]
+
+    @property
+    def heap_bytes(self) -> int:
+        """Bytes of the planned heaps this binding placed its temporaries in."""
+        return self._memory()[0]
+
+    @property
+    def workspace_bytes(self) -> int:
+        """Bytes of device workspace the binding gave its library kernels."""
+        return self._memory()[1]
+
+    @property
+    def bind_allocations(self) -> int:
+        """Device allocations the bind made (0 for a static binding)."""
+        return self._memory()[2]
+
     @property
     def node_count(self) -> int:
         """Dispatches in the bound plan (including an overlap-triggered fallback)."""

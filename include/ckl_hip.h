@@ -184,6 +184,10 @@ uint64_t ckl_invocation_node_count(ckl_invocation *invocation);
 int ckl_invocation_rebind(ckl_invocation *invocation, const ckl_argument *arguments, size_t count);
 /* Graph executables this invocation has instantiated so far (modes 1-4). */
 int ckl_invocation_graph_instantiations(ckl_invocation *invocation, uint64_t *count);
+/* Device memory of the binding (no reference counterpart; the reference reports heap bytes from
+ * the plan text): out[0] planned heap bytes, out[1] library-kernel workspace bytes, out[2] device
+ * allocations the bind made (0 for ckl_bind_static). */
+int ckl_invocation_memory(ckl_invocation *invocation, uint64_t out[3]);
 /* Independent requests (replaces the thread-pool burst of benchmarks/decoder/experiment.py:53-70,
  * one native benchmark call per request thread): `iterations` runs of `batch` steps of each of
  * `count` distinct invocations of one device in `mode`, every invocation on its own stream, all
