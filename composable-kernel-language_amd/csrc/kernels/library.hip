@@ -1020,11 +1020,21 @@ __device__ __forceinline__ float score_scalar(const float *q, const float *key, 
 // the row is summed over its G lanes (group_sum), so with 8-lane groups a row costs three DPP
 // steps instead of a 32-lane butterfly. A wave load covers 64/G rows; a lane keeps kScoreBatch
 // pieces in flight (kScoreBatch/P rows).
-__device__ __forceinline__ int score_pieces(int D) { return D <= 32 ? 1 : D <= 64 ? 2 : 4; }
+__device__ __forceinline__ bool score_groups(int D, int P) {   // G = D/(4P) lanes a row: a power of two
+  const int G = D / (4 * P);
+  return G > 0 && G * 4 * P == D && (G & (G - 1)) == 0;
+}
+// P = 1, 2, 4 for D <= 32, <= 64, larger (8-lane groups for D = 64 and 128); a D those leave
+// without power-of-two groups takes the smallest P that gives them (D = 96: P = 3, 8 lanes).
+__device__ __forceinline__ int score_pieces(int D) {
+  const int preferred = D <= 32 ? 1 : D <= 64 ? 2 : 4;
+  if (score_groups(D, preferred)) return preferred;
+  for (int P = 1; P <= 4; ++P)
+    if (score_groups(D, P)) return P;
+  return preferred;
+}
 __device__ __forceinline__ bool scores_vector_layout(int D) {
-  if ((D & 3) || D > 256) return false;
-  const int P = score_pieces(D), G = D / (4 * P);
-  return G * 4 * P == D && (G & (G - 1)) == 0;        // G lanes a row: a power of two
+  return !(D & 3) && D <= 256 && score_groups(D, score_pieces(D));
 }
 // Partial dot product of a lane's P pieces of q and of one key row.
 template <int P> __device__ __forceinline__ float dot_pieces(const float4 (&q)[P], const float4 *k) {
@@ -1096,6 +1106,7 @@ template <bool NT> __device__ void attention_scores_body(const ScoresArgs &a, in
     switch (score_pieces(a.D)) {
       case 1: attention_scores_rows<NT, 1>(a, q, keys, scores, w0, w1); break;
       case 2: attention_scores_rows<NT, 2>(a, q, keys, scores, w0, w1); break;
+      case 3: attention_scores_rows<NT, 3>(a, q, keys, scores, w0, w1); break;
       default: attention_scores_rows<NT, 4>(a, q, keys, scores, w0, w1); break;
     }
   } else {
@@ -1409,6 +1420,7 @@ __device__ void attention_scores__softmax__attention_values_body(const Attention
   switch (score_pieces(a.scores.D)) {
     case 1: attention_chain_row<NT, 1>(a.scores, a.softmax, a.values, bh, q, p, rowScores, none, false); break;
     case 2: attention_chain_row<NT, 2>(a.scores, a.softmax, a.values, bh, q, p, rowScores, none, false); break;
+    case 3: attention_chain_row<NT, 3>(a.scores, a.softmax, a.values, bh, q, p, rowScores, none, false); break;
     default: attention_chain_row<NT, 4>(a.scores, a.softmax, a.values, bh, q, p, rowScores, none, false); break;
   }
 }
@@ -1478,6 +1490,7 @@ template <bool NT> __device__ void rope_attention_stream(const RopeAttentionChai
   switch (score_pieces(a.scores.D)) {
     case 1: rope_attention_rows<NT, 1>(a, block); break;
     case 2: rope_attention_rows<NT, 2>(a, block); break;
+    case 3: rope_attention_rows<NT, 3>(a, block); break;
     default: rope_attention_rows<NT, 4>(a, block); break;
   }
 }

@@ -413,19 +413,30 @@ std::unique_ptr<GraphExec> explicitGraph(const Plan &plan, const std::vector<Uni
     std::sort(preds[u].begin(), preds[u].end());
     preds[u].erase(std::unique(preds[u].begin(), preds[u].end()), preds[u].end());
   }
-  // reach[u]: units that u depends on, directly or not (bit sets over unit indices).
-  const size_t words = (n + 63) / 64;
+  // reach[u]: the units in [u - span, u) that u depends on, directly or not, where span is the
+  // longest distance from a unit to a predecessor. That window suffices: a predecessor p of u is
+  // redundant when a later predecessor q reaches it, and then q - span <= u - span <= p < q. A
+  // repeated plan's edges reach at most one step back, so the sets stay a few words long however
+  // many steps one graph holds (dense sets would cost n^2/8 bytes).
+  size_t span = 1;
+  for (size_t u = 0; u < n; ++u)
+    if (!preds[u].empty()) span = std::max(span, u - preds[u].front());
+  const size_t words = span / 64 + 2;
+  auto base = [&](size_t u) { return (u > span ? u - span : 0) / 64; };   // first word of u's window
   std::vector<uint64_t> reach(n * words, 0);
   std::vector<std::vector<size_t>> reduced(n);
   for (size_t u = 0; u < n; ++u) {
     uint64_t *mine = &reach[u * words];
+    const size_t first = base(u);
     // A predecessor is kept when no later predecessor already reaches it (scan in descending order).
     for (auto it = preds[u].rbegin(); it != preds[u].rend(); ++it) {
-      size_t p = *it;
-      if (!(mine[p / 64] >> (p % 64) & 1)) reduced[u].push_back(p);
-      mine[p / 64] |= uint64_t(1) << (p % 64);
+      const size_t p = *it;
+      uint64_t &word = mine[p / 64 - first];
+      if (!(word >> (p % 64) & 1)) reduced[u].push_back(p);
+      word |= uint64_t(1) << (p % 64);
       const uint64_t *theirs = &reach[p * words];
-      for (size_t w = 0; w < words; ++w) mine[w] |= theirs[w];
+      const size_t from = base(p);                 // <= first: p's window starts no later than u's
+      for (size_t w = first; w <= (p ? (p - 1) / 64 : 0) && w - from < words; ++w) mine[w - first] |= theirs[w - from];
     }
   }
   check(hipGraphCreate(&out->graph, 0), "hipGraphCreate");
@@ -490,10 +501,14 @@ constexpr int kMaxStaticDevices = 64;
 std::array<std::atomic<uint64_t>, kMaxStaticDevices> staticEpochs{};
 } // namespace
 
-void Invocation::validate(int mode, uint64_t batch) const {
+void Invocation::requireCurrent() const {
   if (staticArena && staticEpochs[size_t(device->ordinal)].load() != epoch)
     throw std::invalid_argument("this invocation's static arena was taken over by a later ckl_bind_static on the same "
                                 "device; bind it again");
+}
+
+void Invocation::validate(int mode, uint64_t batch) const {
+  requireCurrent();
   if (mode < kOrdinary || mode > kInferredStream || !batch || plan.nodes.empty() ||
       batch > 1000000 / plan.nodes.size())
     throw std::invalid_argument("invalid execution mode or batch exceeds one million kernel nodes");
@@ -699,7 +714,14 @@ uint64_t Invocation::graphInstantiations() {
 
 void Invocation::rebind(const std::vector<Argument> &arguments) {
   std::lock_guard<std::mutex> lock(runMutex);
+  requireCurrent();
   if (!requested) throw std::invalid_argument("this invocation was not bound from program arguments");
+  // A resource bound from an address the host entry did not take from the packed program
+  // arguments cannot be followed to its new buffer.
+  for (size_t id = 0; id < externalResources.size(); ++id)
+    if (externalResources[id] && (id >= resourceArgument.size() || resourceArgument[id] < 0))
+      throw std::invalid_argument("resource " + std::to_string(id) + " was bound from an address outside the packed "
+                                  "program arguments, so a rebind cannot move it; bind again");
   std::vector<uint64_t> addresses, scalars;
   std::vector<std::shared_ptr<Buffer>> keep;
   packArguments(*requested, device.get(), arguments, addresses, scalars, keep);
@@ -816,6 +838,7 @@ std::array<uint64_t, 3> Invocation::memory() const {
 
 double Invocation::timeNode(size_t index, uint64_t iterations) {
   std::lock_guard<std::mutex> lock(runMutex);
+  requireCurrent();
   return timeLaunch(plan.nodes.at(index).launch, iterations);
 }
 
@@ -1004,7 +1027,9 @@ extern "C" void ckl_resource(void *frame, uint64_t id, uint64_t heap, uint64_t o
     if (f.resources.size() <= id) f.resources.resize(id + 1);
     if (f.temporaryResources.size() <= id) f.temporaryResources.resize(id + 1, false);
     if (f.resourceArgument.size() <= id) f.resourceArgument.resize(id + 1, -1);
+    if (f.externalResources.size() <= id) f.externalResources.resize(id + 1, false);
     f.temporaryResources[id] = !external;
+    f.externalResources[id] = external != nullptr;
     if (external) {
       f.resources[id] = *static_cast<uint64_t *>(external);
       // Which program argument the resource is: the entry passes the packed address's location.

@@ -162,6 +162,7 @@ struct Invocation {
   std::vector<std::shared_ptr<Buffer>> workspaces;  // private library-kernel workspaces (zeroed at bind)
   std::vector<uint64_t> resources;
   std::vector<bool> temporaryResources;             // resource id -> placed in a heap
+  std::vector<bool> externalResources;              // resource id -> a program argument's address
   Plan plan;
   hipModule_t module = nullptr;                     // current module during plan construction
   Launch pending;
@@ -227,6 +228,7 @@ struct Invocation {
 private:
   friend std::array<double, 2> runConcurrently(const std::vector<Invocation *> &, int, uint64_t, uint64_t, bool);
   void validate(int mode, uint64_t batch) const;
+  void requireCurrent() const;                      // refuses a superseded static binding
   GraphExec &inferredUnits();
   double timeLaunch(const Launch &launch, uint64_t iterations);
   GraphExec &graphFor(int mode, uint64_t batch);

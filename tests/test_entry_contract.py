@@ -173,3 +173,83 @@ def test_entry_program_runs_in_every_mode(device):
         lib.ckl_program_release(program)
         for b in buffers:
             lib.ckl_buffer_release(b)
+
+
+class CopiedAddressEntry(JoinEntry):
+    """JoinEntry, except that resource 0 is declared from the entry's own copy of the first
+    argument's address rather than from the packed argument array."""
+
+    def __call__(self, packed):
+        args = ctypes.cast(ctypes.cast(packed, ctypes.POINTER(ctypes.c_void_p))[1],
+                           ctypes.POINTER(ctypes.POINTER(ctypes.c_void_p)))[0]
+        self.copy = ctypes.c_uint64(ctypes.cast(args[0], ctypes.POINTER(ctypes.c_uint64))[0])
+        saved = args[0]
+        args[0] = ctypes.cast(ctypes.pointer(self.copy), ctypes.c_void_p)
+        try:
+            super().__call__(packed)
+        finally:
+            args[0] = saved
+
+
+def rebind(invocation, arguments):
+    packed = (_native.Argument * len(arguments))()
+    for k, (kind, value) in enumerate(arguments):
+        packed[k].kind = kind
+        if kind == 0:
+            packed[k].buffer = value
+        elif kind in (1, 2):
+            packed[k].integer = value
+        else:
+            packed[k].real = value
+    _native.check(_native.native().ckl_invocation_rebind(invocation, packed, len(arguments)))
+
+
+@pytest.mark.gpu
+def test_rebind_follows_packed_arguments_and_refuses_copied_addresses(device):
+    """A rebind moves resources the entry declared from the packed argument array to the new
+    buffers; one declared from an address the entry copied elsewhere cannot be followed, so the
+    rebind is refused with ValueError instead of leaving graphs that write freed memory."""
+    lib = _native.native()
+    dev = device._native_resource.pointer
+
+    def buffers():
+        out = []
+        for values in (np.ones(32, np.float32), np.full(32, 3.0, np.float32), np.zeros(32, np.float32)):
+            handle = ctypes.c_void_p()
+            _native.check(lib.ckl_buffer_alloc(dev, 128, ctypes.byref(handle)))
+            _native.check(lib.ckl_buffer_copy_from_host(handle, values.ctypes.data, 128))
+            out.append(handle.value)
+        return out
+
+    first, second = buffers(), buffers()
+    scalars = [(1, 32), (3, 1.25), (4, -2.5), (2, -1234567890123)]
+    result = np.empty(32, np.float32)
+    held = []
+    try:
+        for kind in (JoinEntry, CopiedAddressEntry):
+            entry = kind(KERNEL.read_bytes())
+            program = from_entry(entry.function)
+            invocation = bind(program, dev, [(0, b) for b in first] + scalars)
+            held.append((invocation, program, entry))
+            _native.check(lib.ckl_invocation_run(invocation, 1, 1))
+            _native.check(lib.ckl_buffer_copy_to_host(first[2], result.ctypes.data, 128))
+            assert np.all(result == np.float32(2.21875)), kind.__name__
+            if kind is JoinEntry:
+                rebind(invocation, [(0, b) for b in second] + scalars)
+                _native.check(lib.ckl_invocation_run(invocation, 1, 1))
+                _native.check(lib.ckl_buffer_copy_to_host(second[2], result.ctypes.data, 128))
+                assert np.all(result == np.float32(2.21875))
+            else:
+                with pytest.raises(ValueError, match="outside the packed"):
+                    rebind(invocation, [(0, b) for b in second] + scalars)
+                # The refused rebind left the binding as it was.
+                _native.check(lib.ckl_buffer_copy_from_host(first[2], np.zeros(32, np.float32).ctypes.data, 128))
+                _native.check(lib.ckl_invocation_run(invocation, 1, 1))
+                _native.check(lib.ckl_buffer_copy_to_host(first[2], result.ctypes.data, 128))
+                assert np.all(result == np.float32(2.21875))
+    finally:
+        for invocation, program, _ in held:
+            lib.ckl_invocation_release(invocation)
+            lib.ckl_program_release(program)
+        for b in first + second:
+            lib.ckl_buffer_release(b)

@@ -90,6 +90,9 @@ def test_static_bind_matches_ckl_bind_twice(device, stream):
     try:
         with pytest.raises(ValueError, match="taken over"):
             run(first, 1)
+        with pytest.raises(ValueError, match="taken over"):
+            average = ctypes.c_double()
+            _native.check(lib.ckl_invocation_time_node(first, 0, 1, ctypes.byref(average)))
         run(second, 1)
     finally:
         lib.ckl_invocation_release(first)
@@ -112,3 +115,37 @@ def test_static_bind_refuses_programs_beyond_the_arena(device, stream):
         _native.check(_native.native().ckl_bind_static(compiled._native_resource.pointer,
                                                        device._native_resource.pointer, packed, 3, stream,
                                                        ctypes.byref(handle)))
+
+
+def memory(handle):
+    out = (ctypes.c_uint64 * 3)()
+    _native.check(_native.native().ckl_invocation_memory(handle, out))
+    return list(out)
+
+
+def test_static_bind_allocates_no_device_memory(device, stream):
+    """A static bind after a warm-up one (same program, same stream) makes no device allocation:
+    the binding reports none, and the device's free memory is the same before and after it."""
+    hip = ctypes.CDLL("libamdhip64.so")
+    lib = _native.native()
+    initial, _ = oracle.make_inputs(SMALLER, 123, init="baseline")
+    session = DecoderSession(SMALLER, device, arrays=initial)
+    assert session.invocations[True].bind_allocations > 0
+    program, arguments = session.programs[True], session.state.arguments()
+    warm = bind_static(program, device, arguments, stream)
+    hip.hipStreamSynchronize(ctypes.c_void_p(stream))
+    free, total = ctypes.c_size_t(), ctypes.c_size_t()
+    assert hip.hipMemGetInfo(ctypes.byref(free), ctypes.byref(total)) == 0
+    before = free.value
+    handle = bind_static(program, device, arguments, stream)
+    hip.hipStreamSynchronize(ctypes.c_void_p(stream))
+    assert hip.hipMemGetInfo(ctypes.byref(free), ctypes.byref(total)) == 0
+    try:
+        assert free.value == before
+        heap, workspace, allocations = memory(handle)
+        assert allocations == 0 and heap > 0 and workspace > 0
+        assert memory(warm)[:2] == [heap, workspace]
+    finally:
+        lib.ckl_invocation_release(warm)
+        lib.ckl_invocation_release(handle)
+
