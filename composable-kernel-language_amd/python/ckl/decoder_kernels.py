@@ -1,194 +1,217 @@
-"""The decoder kernel set: the CKL kernel bodies that the gfx950 library implements by hand.
+"""Contract bodies of the hand-written gfx950 kernels (csrc/kernels/library.hip).
 
-These are the kernels of the reference's decoder workload (benchmarks/decoder/workloads.py:33-188)
-and of its vector pipeline example (examples/vector_pipeline.py:11-16), restated as the contract
-the library is a drop-in for: a kernel specialisation is served by the library exactly when its
-IR, printed canonically, equals the IR of the matching body here specialised the same way
-(ckl.library). Programs may launch these definitions directly (programs/decoder.py does) or
-define bodies of their own; only the IR decides.
+A CKL kernel specialisation runs on a library kernel exactly when its IR, printed canonically
+(no names: SSA numbers, argument positions and concrete types only), equals the IR of the body
+below with the same name, specialised to the same signature (ckl.library). The bodies therefore
+fix the operation sequence of the kernels the decoder benchmark launches (the reference's
+benchmarks/decoder/workloads.py:33-188) and of the vector-pipeline example's `update`
+(examples/vector_pipeline.py:11-16); tests/golden/workload_ir.json records the canonical IR of
+those reference kernels for every specialisation the decode program uses, and
+tests/test_contract_ir.py checks these bodies against it. Everything else here (names, aliases,
+layout of the source) is this package's own.
+
+Threads: x is the innermost index of the written element, y and z the outer ones; a thread
+outside the output's extent does nothing. Arithmetic is f32 in the order written.
 """
 from __future__ import annotations
 
 import ckl
 
-_B, _C, _L, _A, _T, _D, _V, _R = [ckl.dim(n) for n in ("B", "C", "L", "A", "T", "D", "V", "R")]
-_W, _I, _O, _N = [ckl.dim(n) for n in ("W", "I", "O", "N")]
-_Hidden = ckl.Buffer[ckl.f32, (_B, _C)]
-_Rows = ckl.Buffer[ckl.f32, (_B,)]
-_Tokens = ckl.Buffer[ckl.i32, (_B,)]
-_Position = ckl.Buffer[ckl.i32, (1,)]
-_History = ckl.Buffer[ckl.i32, (_T, _B)]
-_Table = ckl.Buffer[ckl.f32, (_V, _C)]
-_Gain = ckl.Buffer[ckl.f32, (_L, _C)]
-_Cache = ckl.Buffer[ckl.f32, (_L, _B, _A, _T, _D)]
-_SinCos = ckl.Buffer[ckl.f32, (_T, _R, 2)]
-_Scores = ckl.Buffer[ckl.f32, (_B, _A, _T)]
-_Logits = ckl.Buffer[ckl.f32, (_B, _V)]
-_In = ckl.Buffer[ckl.f32, (_B, _I)]
-_Out = ckl.Buffer[ckl.f32, (_B, _O)]
-_Matrix = ckl.Buffer[ckl.f32, (_W, _I, _O)]
-_Vector = ckl.Buffer[ckl.f32, (_N,)]
+BATCH, WIDTH, DEPTH, HEADS, SLOTS, HEAD, VOCAB, PAIRS = (
+    ckl.dim(n) for n in ("batch", "width", "depth", "heads", "slots", "head", "vocab", "pairs"))
+STACK, FAN_IN, FAN_OUT, LENGTH = (ckl.dim(n) for n in ("stack", "fan_in", "fan_out", "length"))
+
+Activations = ckl.Buffer[ckl.f32, (BATCH, WIDTH)]        # one row of WIDTH features per request
+PerRequest = ckl.Buffer[ckl.f32, (BATCH,)]
+TokenIds = ckl.Buffer[ckl.i32, (BATCH,)]
+Cursor = ckl.Buffer[ckl.i32, (1,)]                        # the decode position
+Emitted = ckl.Buffer[ckl.i32, (SLOTS, BATCH)]             # generated tokens by position
+Vocabulary = ckl.Buffer[ckl.f32, (VOCAB, WIDTH)]
+Gains = ckl.Buffer[ckl.f32, (DEPTH, WIDTH)]
+KVCache = ckl.Buffer[ckl.f32, (DEPTH, BATCH, HEADS, SLOTS, HEAD)]
+Rotations = ckl.Buffer[ckl.f32, (SLOTS, PAIRS, 2)]        # (cos, sin) per position and pair
+HeadRows = ckl.Buffer[ckl.f32, (BATCH, HEADS, SLOTS)]     # one value per cached position
+Logits = ckl.Buffer[ckl.f32, (BATCH, VOCAB)]
+Inputs = ckl.Buffer[ckl.f32, (BATCH, FAN_IN)]
+Outputs = ckl.Buffer[ckl.f32, (BATCH, FAN_OUT)]
+Weights = ckl.Buffer[ckl.f32, (STACK, FAN_IN, FAN_OUT)]  # one matrix per layer
+Flat = ckl.Buffer[ckl.f32, (LENGTH,)]
 
 
 @ckl.kernel
-def embedding(tokens: _Tokens, table: _Table, dst: _Hidden) -> None:
-    c = ckl.global_id(0)
-    b = ckl.global_id(1)
-    if c < _C:
-        token = ckl.cast(tokens[b], ckl.index)
-        dst[b, c] = table[token, c]
+def embedding(ids: TokenIds, table: Vocabulary, out: Activations) -> None:
+    """out[r, :] = table[ids[r], :]."""
+    col = ckl.global_id(0)
+    row = ckl.global_id(1)
+    if col < WIDTH:
+        entry = ckl.cast(ids[row], ckl.index)
+        out[row, col] = table[entry, col]
 
 
 @ckl.kernel
-def rms_stats(x: _Hidden, inv: _Rows, epsilon: ckl.f32) -> None:
-    b = ckl.global_id(0)
-    if b < _B:
-        total = 0.0
-        for c in range(_C):
-            total = total + x[b, c] * x[b, c]
-        inv[b] = ckl.rsqrt(total / _C + epsilon)
+def rms_stats(rows: Activations, inverse: PerRequest, eps: ckl.f32) -> None:
+    """inverse[r] = 1 / sqrt(mean of rows[r, :]^2 + eps), one thread a row, columns in order."""
+    row = ckl.global_id(0)
+    if row < BATCH:
+        squares = 0.0
+        for col in range(WIDTH):
+            squares = squares + rows[row, col] * rows[row, col]
+        inverse[row] = ckl.rsqrt(squares / WIDTH + eps)
 
 
 @ckl.kernel
-def rms_apply(x: _Hidden, inv: _Rows, gain: _Gain, dst: _Hidden, layer: ckl.constexpr[ckl.index]) -> None:
-    c = ckl.global_id(0)
-    b = ckl.global_id(1)
-    if c < _C:
-        dst[b, c] = x[b, c] * inv[b] * gain[layer, c]
+def rms_apply(rows: Activations, inverse: PerRequest, gains: Gains, out: Activations,
+              which: ckl.constexpr[ckl.index]) -> None:
+    """out[r, c] = (rows[r, c] * inverse[r]) * gains[which, c]."""
+    col = ckl.global_id(0)
+    row = ckl.global_id(1)
+    if col < WIDTH:
+        out[row, col] = rows[row, col] * inverse[row] * gains[which, col]
 
 
 @ckl.kernel
-def linear(x: _In, weight: _Matrix, dst: _Out, layer: ckl.constexpr[ckl.index]) -> None:
-    o = ckl.global_id(0)
-    b = ckl.global_id(1)
-    if o < _O:
-        total = 0.0
-        for i in range(_I):
-            total = total + x[b, i] * weight[layer, i, o]
-        dst[b, o] = total
+def linear(source: Inputs, matrices: Weights, out: Outputs, which: ckl.constexpr[ckl.index]) -> None:
+    """out[r, o] = sum over i (in order) of source[r, i] * matrices[which, i, o]."""
+    col = ckl.global_id(0)
+    row = ckl.global_id(1)
+    if col < FAN_OUT:
+        acc = 0.0
+        for k in range(FAN_IN):
+            acc = acc + source[row, k] * matrices[which, k, col]
+        out[row, col] = acc
 
 
 @ckl.kernel
-def rope(src: _Hidden, table: _SinCos, position: _Position, dst: _Hidden) -> None:
-    r = ckl.global_id(0)
-    h = ckl.global_id(1)
-    b = ckl.global_id(2)
-    if r < _R:
-        p = ckl.cast(position[0], ckl.index)
-        c = h * (2 * _R) + 2 * r
-        first = src[b, c]
-        second = src[b, c + 1]
-        cosine = table[p, r, 0]
-        sine = table[p, r, 1]
-        dst[b, c] = first * cosine - second * sine
-        dst[b, c + 1] = first * sine + second * cosine
+def rope(source: Activations, rotations: Rotations, cursor: Cursor, out: Activations) -> None:
+    """Rotates feature pair (2j, 2j+1) of head h by the angle of pair j at the cursor."""
+    pair = ckl.global_id(0)
+    head = ckl.global_id(1)
+    row = ckl.global_id(2)
+    if pair < PAIRS:
+        at = ckl.cast(cursor[0], ckl.index)
+        even = head * (2 * PAIRS) + 2 * pair
+        re = source[row, even]
+        im = source[row, even + 1]
+        cos = rotations[at, pair, 0]
+        sin = rotations[at, pair, 1]
+        out[row, even] = re * cos - im * sin
+        out[row, even + 1] = re * sin + im * cos
 
 
 @ckl.kernel
-def append_kv(k: _Hidden, v: _Hidden, kc: _Cache, vc: _Cache, position: _Position,
-              layer: ckl.constexpr[ckl.index]) -> None:
-    d = ckl.global_id(0)
-    h = ckl.global_id(1)
-    b = ckl.global_id(2)
-    if d < _D:
-        p = ckl.cast(position[0], ckl.index)
-        kc[layer, b, h, p, d] = k[b, h * _D + d]
-        vc[layer, b, h, p, d] = v[b, h * _D + d]
+def append_kv(keys: Activations, values: Activations, key_cache: KVCache, value_cache: KVCache, cursor: Cursor,
+              which: ckl.constexpr[ckl.index]) -> None:
+    """Stores head h's key and value features of every request at the cursor's slot."""
+    lane = ckl.global_id(0)
+    head = ckl.global_id(1)
+    row = ckl.global_id(2)
+    if lane < HEAD:
+        at = ckl.cast(cursor[0], ckl.index)
+        key_cache[which, row, head, at, lane] = keys[row, head * HEAD + lane]
+        value_cache[which, row, head, at, lane] = values[row, head * HEAD + lane]
 
 
 @ckl.kernel
-def attention_scores(q: _Hidden, kc: _Cache, position: _Position, scores: _Scores,
-                     scale: ckl.f32, layer: ckl.constexpr[ckl.index]) -> None:
-    t = ckl.global_id(0)
-    h = ckl.global_id(1)
-    b = ckl.global_id(2)
-    end = ckl.cast(position[0], ckl.index) + 1
-    if t < end:
-        total = 0.0
-        for d in range(_D):
-            total = total + q[b, h * _D + d] * kc[layer, b, h, t, d]
-        scores[b, h, t] = total * scale
+def attention_scores(query: Activations, key_cache: KVCache, cursor: Cursor, out: HeadRows, scale: ckl.f32,
+                     which: ckl.constexpr[ckl.index]) -> None:
+    """out[r, h, s] = (query head h . cached key s) * scale for every slot s up to the cursor."""
+    slot = ckl.global_id(0)
+    head = ckl.global_id(1)
+    row = ckl.global_id(2)
+    upto = ckl.cast(cursor[0], ckl.index) + 1
+    if slot < upto:
+        dot = 0.0
+        for lane in range(HEAD):
+            dot = dot + query[row, head * HEAD + lane] * key_cache[which, row, head, slot, lane]
+        out[row, head, slot] = dot * scale
 
 
 @ckl.kernel
-def softmax(scores: _Scores, position: _Position, probs: _Scores) -> None:
-    b = ckl.global_id(0)
-    h = ckl.global_id(1)
-    if b < _B:
-        end = ckl.cast(position[0], ckl.index) + 1
-        maximum = scores[b, h, 0]
-        for t in range(1, end):
-            value = scores[b, h, t]
-            maximum = ckl.select(value > maximum, value, maximum)
-        total = 0.0
-        for t in range(end):
-            total = total + ckl.exp(scores[b, h, t] - maximum)
-        for t in range(end):
-            probs[b, h, t] = ckl.exp(scores[b, h, t] - maximum) / total
+def softmax(logits: HeadRows, cursor: Cursor, out: HeadRows) -> None:
+    """out[r, h, :] = exp(x - max) / sum(exp(x - max)) over slots 0..cursor; the maximum is a
+    strict `>` scan from slot 0, the sum is taken in slot order."""
+    row = ckl.global_id(0)
+    head = ckl.global_id(1)
+    if row < BATCH:
+        upto = ckl.cast(cursor[0], ckl.index) + 1
+        peak = logits[row, head, 0]
+        for slot in range(1, upto):
+            candidate = logits[row, head, slot]
+            peak = ckl.select(candidate > peak, candidate, peak)
+        norm = 0.0
+        for slot in range(upto):
+            norm = norm + ckl.exp(logits[row, head, slot] - peak)
+        for slot in range(upto):
+            out[row, head, slot] = ckl.exp(logits[row, head, slot] - peak) / norm
 
 
 @ckl.kernel
-def attention_values(probs: _Scores, vc: _Cache, position: _Position, dst: _Hidden,
-                     layer: ckl.constexpr[ckl.index]) -> None:
-    d = ckl.global_id(0)
-    h = ckl.global_id(1)
-    b = ckl.global_id(2)
-    if d < _D:
-        end = ckl.cast(position[0], ckl.index) + 1
-        total = 0.0
-        for t in range(end):
-            total = total + probs[b, h, t] * vc[layer, b, h, t, d]
-        dst[b, h * _D + d] = total
+def attention_values(weights: HeadRows, value_cache: KVCache, cursor: Cursor, out: Activations,
+                     which: ckl.constexpr[ckl.index]) -> None:
+    """out[r, h*HEAD + d] = sum over slots 0..cursor (in order) of weight * cached value."""
+    lane = ckl.global_id(0)
+    head = ckl.global_id(1)
+    row = ckl.global_id(2)
+    if lane < HEAD:
+        upto = ckl.cast(cursor[0], ckl.index) + 1
+        acc = 0.0
+        for slot in range(upto):
+            acc = acc + weights[row, head, slot] * value_cache[which, row, head, slot, lane]
+        out[row, head * HEAD + lane] = acc
 
 
 @ckl.kernel
-def add(x: _Hidden, y: _Hidden, dst: _Hidden) -> None:
-    c = ckl.global_id(0)
-    b = ckl.global_id(1)
-    if c < _C:
-        dst[b, c] = x[b, c] + y[b, c]
+def add(lhs: Activations, rhs: Activations, out: Activations) -> None:
+    col = ckl.global_id(0)
+    row = ckl.global_id(1)
+    if col < WIDTH:
+        out[row, col] = lhs[row, col] + rhs[row, col]
 
 
 @ckl.kernel
-def silu(src: _In, dst: _In) -> None:
+def silu(source: Inputs, out: Inputs) -> None:
+    """out = x / (1 + exp(-x))."""
+    col = ckl.global_id(0)
+    row = ckl.global_id(1)
+    if col < FAN_IN:
+        x = source[row, col]
+        out[row, col] = x / (1.0 + ckl.exp(-x))
+
+
+@ckl.kernel
+def multiply(lhs: Inputs, rhs: Inputs, out: Inputs) -> None:
+    col = ckl.global_id(0)
+    row = ckl.global_id(1)
+    if col < FAN_IN:
+        out[row, col] = lhs[row, col] * rhs[row, col]
+
+
+@ckl.kernel
+def greedy(logits: Logits, ids: TokenIds, emitted: Emitted, cursor: Cursor) -> None:
+    """ids[r] = emitted[cursor, r] = the first index of the largest logit of row r (a strict `>`
+    scan from index 0, so NaN never wins and ties keep the earlier index)."""
+    row = ckl.global_id(0)
+    if row < BATCH:
+        best = logits[row, 0]
+        choice = ckl.cast(row, ckl.i32) * 0
+        for index in range(1, VOCAB):
+            candidate = logits[row, index]
+            better = candidate > best
+            choice = ckl.select(better, ckl.cast(index, ckl.i32), choice)
+            best = ckl.select(better, candidate, best)
+        at = ckl.cast(cursor[0], ckl.index)
+        ids[row] = choice
+        emitted[at, row] = choice
+
+
+@ckl.kernel
+def advance(cursor: Cursor) -> None:
+    cursor[0] = cursor[0] + 1
+
+
+@ckl.kernel
+def update(source: Flat, out: Flat, shift: ckl.f32) -> None:
+    """out[i] = source[i] + shift."""
     i = ckl.global_id(0)
-    b = ckl.global_id(1)
-    if i < _I:
-        value = src[b, i]
-        dst[b, i] = value / (1.0 + ckl.exp(-value))
-
-
-@ckl.kernel
-def multiply(x: _In, y: _In, dst: _In) -> None:
-    i = ckl.global_id(0)
-    b = ckl.global_id(1)
-    if i < _I:
-        dst[b, i] = x[b, i] * y[b, i]
-
-
-@ckl.kernel
-def greedy(logits: _Logits, tokens: _Tokens, history: _History, position: _Position) -> None:
-    b = ckl.global_id(0)
-    if b < _B:
-        maximum = logits[b, 0]
-        winner = ckl.cast(b, ckl.i32) * 0
-        for v in range(1, _V):
-            score = logits[b, v]
-            wins = score > maximum
-            winner = ckl.select(wins, ckl.cast(v, ckl.i32), winner)
-            maximum = ckl.select(wins, score, maximum)
-        p = ckl.cast(position[0], ckl.index)
-        tokens[b] = winner
-        history[p, b] = winner
-
-
-@ckl.kernel
-def advance(position: _Position) -> None:
-    position[0] = position[0] + 1
-
-
-@ckl.kernel
-def update(src: _Vector, dst: _Vector, bias: ckl.f32) -> None:
-    i = ckl.global_id(0)
-    if i < src.shape[0]:
-        dst[i] = src[i] + bias
+    if i < source.shape[0]:
+        out[i] = source[i] + shift

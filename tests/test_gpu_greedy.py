@@ -10,8 +10,8 @@ import pytest
 
 import ckl
 from oracle import decoder as oracle
-from ckl.decoder_kernels import _B, advance, greedy, linear
-from ckl.decoder_kernels import _History as History, _Logits as Logits, _Position as Position, _Tokens as Tokens
+from ckl.decoder_kernels import BATCH, advance, greedy, linear
+from ckl.decoder_kernels import Cursor as Position, Emitted as History, Logits, TokenIds as Tokens
 from test_oracle_decoder import edge_rows
 
 pytestmark = pytest.mark.gpu
@@ -19,7 +19,7 @@ pytestmark = pytest.mark.gpu
 
 @ckl.program
 def pick(logits: Logits, tokens: Tokens, history: History, position: Position) -> None:
-    ckl.launch(greedy, logits, tokens, history, position, grid=(ckl.cdiv(_B, 32),), block=(32,))
+    ckl.launch(greedy, logits, tokens, history, position, grid=(ckl.cdiv(BATCH, 32),), block=(32,))
     ckl.launch(advance, position, grid=(1,), block=(1,))
 
 
