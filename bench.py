@@ -192,9 +192,11 @@ def time_variants(session, c, steps, warmup, expected, log_prefix, only=None):
     return table
 
 
-def heap_bytes(program) -> int:
+def heap_bytes(program, op='"ckl_exec.heap"') -> int:
+    """Bytes of the plan's temporaries' heaps (or, with op='"ckl_exec.workspace_heap"', of its
+    library-workspace heap), read from the executable plan text."""
     return sum(int(line.split("bytes = ")[1].split(" ")[0]) for line in program.executable_ir.splitlines()
-               if '"ckl_exec.heap"' in line)
+               if op in line)
 
 
 def run_config(name, c, args, device, checker):
@@ -235,8 +237,10 @@ def run_config(name, c, args, device, checker):
                   inferred_reuse_over_capture_reuse=ratio("capture_reuse", "inferred_reuse"),
                   batched_branches_over_batched_capture=ratio("batched_capture", "batched_branches"),
                   scratch_bytes={"reuse_off": heap["False"], "reuse_on": heap["True"]},
-                  workspace_bytes={"reuse_off": session.invocations[False].workspace_bytes,
-                                   "reuse_on": session.invocations[True].workspace_bytes},
+                  workspace_bytes={"reuse_off": heap_bytes(session.programs[False], '"ckl_exec.workspace_heap"'),
+                                   "reuse_on": heap_bytes(session.programs[True], '"ckl_exec.workspace_heap"')},
+                  bind_allocations={"reuse_off": session.invocations[False].bind_allocations,
+                                    "reuse_on": session.invocations[True].bind_allocations},
                   tokens_per_s=c.batch * 1e6 / step_us,
                   algorithmic_bytes_per_step=mean_bytes,
                   step_hbm_fraction=mean_bytes / (step_us * 1e-6) / HBM_PEAK,
@@ -814,7 +818,7 @@ def measure(args, checker):
                                            "stream_us", "inferred_reuse_us", "batched_inferred_us",
                                            "inferred_over_capture", "branches_over_capture",
                                            "contracted_over_capture", "stream_over_capture", "scratch_bytes",
-                                           "workspace_bytes", "tokens_per_s", "step_hbm_fraction",
+                                           "workspace_bytes", "bind_allocations", "tokens_per_s", "step_hbm_fraction",
                                            "logits_normwise", "runs_verified")},
                    "verification": "every run of every variant against the NumPy decoder (oracle/decoder.py) from "
                                    "the GPU-prefilled state: tokens, history, position exact; logits atol 2e-5 rtol "

@@ -646,6 +646,7 @@ std::optional<Graph> buildGraph(Module &module, Op *function, const std::map<con
       std::vector<planning::GraphEdge> edges;
       for (const auto &[edge, _] : graph.edges) edges.push_back({edge.first, edge.second});
       auto planned = planning::MemoryPlanner(reuseStorage).tryPlan(graph.nodes.size(), edges, plannerResources);
+      graph.reuseStorage = reuseStorage;
       if (planned) { graph.plan = *planned.value; graph.planned = true; }
       else graph.unavailableReason = planned.error;
     }
@@ -863,6 +864,17 @@ std::string ExecPlan::print() const {
     if (r.kind == "temporary") { e.push_back({"heap", Attr::integer(r.heap)}); e.push_back({"offset", Attr::integer(r.offset)}); }
     out << "    \"ckl_exec.resource\"() <" << Attr::dictOf(e).str() << "> : () -> ()\n";
   }
+  for (const ExecHeap &h : workspaceHeaps)
+    out << "    \"ckl_exec.workspace_heap\"() <" << Attr::dictOf({{"alignment", Attr::integer(h.alignment)},
+                                                                 {"bytes", Attr::integer(h.bytes)},
+                                                                 {"device", Attr::integer(h.device)},
+                                                                 {"id", Attr::integer(h.id)}}).str()
+        << "> : () -> ()\n";
+  for (const ExecWorkspace &w : workspaces)
+    out << "    \"ckl_exec.workspace\"() <" << Attr::dictOf({{"bytes", Attr::integer(w.bytes)}, {"heap", Attr::integer(w.heap)},
+                                                            {"kernel", Attr::integer(w.kernel)}, {"name", Attr::string(w.name)},
+                                                            {"offset", Attr::integer(w.offset)}, {"role", Attr::string(w.role)}}).str()
+        << "> : () -> ()\n";
   for (const ExecKernel &k : kernels) {
     std::vector<Attr> args;
     for (const ExecArgument &a : k.arguments) args.push_back(a.attr());
@@ -875,6 +887,7 @@ std::string ExecPlan::print() const {
         {"shared_memory", Attr::integer(k.sharedMemory)}};
     if (!k.group.empty()) e.push_back({"group", Attr::string(k.group)});
     if (k.workspace) e.push_back({"workspace", Attr::integer(k.workspace)});
+    if (k.partials >= 0) e.push_back({"partials", Attr::integer(k.partials)});
     out << "    \"ckl_exec.kernel\"() <" << Attr::dictOf(e).str() << "> : () -> ()\n";
   }
   out << "  }) : () -> ()\n";
@@ -905,8 +918,39 @@ void ExecPlan::verify() const {
         throw CompileError("'ckl_exec.resource' op placement exceeds its heap");
     }
   }
+  if (workspaceHeaps.size() > 1) throw CompileError("'ckl_exec.workspace_heap' op may appear at most once");
+  for (const ExecHeap &h : workspaceHeaps) {
+    if (h.bytes <= 0 || h.alignment <= 0 || (h.alignment & (h.alignment - 1)) || !heapIds.insert(h.id).second)
+      throw CompileError("'ckl_exec.workspace_heap' op requires a new heap id, positive bytes and power-of-two alignment");
+    heapBytes[h.id] = h.bytes;
+  }
+  std::map<int64_t, std::map<std::string, const ExecWorkspace *>> roles;
+  std::set<std::string> workspaceNames;
+  for (const ExecWorkspace &w : workspaces) {
+    if (!workspaceNames.insert(w.name).second) throw CompileError("'ckl_exec.workspace' op has a duplicate name");
+    if (workspaceHeaps.empty() || w.heap != workspaceHeaps.front().id)
+      throw CompileError("'ckl_exec.workspace' op must be placed in the workspace heap");
+    if (w.role != "state" && w.role != "partials") throw CompileError("'ckl_exec.workspace' op role must be state or partials");
+    if (w.bytes <= 0 || w.offset < 0 || w.offset % 256 || w.offset > heapBytes[w.heap] || w.bytes > heapBytes[w.heap] - w.offset)
+      throw CompileError("'ckl_exec.workspace' op placement exceeds its heap");
+    if (w.name.empty() || byName.count(w.name) || !roles[w.kernel].emplace(w.role, &w).second)
+      throw CompileError("'ckl_exec.workspace' op requires a new name and one placement per kernel and role");
+  }
+  for (const auto &[kernel, _] : roles)
+    if (std::none_of(kernels.begin(), kernels.end(), [&](const ExecKernel &k) { return k.id == kernel; }))
+      throw CompileError("'ckl_exec.workspace' op references an unknown kernel");
   for (const ExecKernel &k : kernels) {
     if (!kernelIds.insert(k.id).second) throw CompileError("'ckl_exec.kernel' op has a duplicate kernel id");
+    if (k.workspace < 0 || k.partials < -1) throw CompileError("'ckl_exec.kernel' op workspace sizes must be non-negative");
+    auto placed = roles.find(k.id);
+    auto bytesOf = [&](const char *role) -> int64_t {
+      if (placed == roles.end() || !placed->second.count(role)) return 0;
+      return placed->second.at(role)->bytes;
+    };
+    if (!workspaceHeaps.empty() && (bytesOf("state") != k.workspace || bytesOf("partials") != std::max<int64_t>(k.partials, 0)))
+      throw CompileError("'ckl_exec.kernel' op workspace sizes do not match its placed workspaces");
+    if (workspaceHeaps.empty() && k.partials > 0)
+      throw CompileError("'ckl_exec.kernel' op with partial planes requires a workspace heap");
     if (k.implementation.empty() || k.artifact.empty() || k.abi.empty() || k.device.empty())
       throw CompileError("'ckl_exec.kernel' op requires implementation, artifact, ABI, and device identities");
     for (const auto *dims : {&k.grid, &k.block})
@@ -957,6 +1001,73 @@ static std::vector<int64_t> dims3(const Attr *a) {
   if (!a) return {};
   std::vector<int64_t> out = a->dense;
   return out;
+}
+
+// Library workspaces (HIP addition, no reference counterpart): one workspace heap, numbered after
+// the plan's heaps, so the temporaries' heaps and offsets stay those of the reference planner.
+// State parts (zero page, completion counters) are laid out one after another at its start and
+// never shared. Partial planes are placed by the storage planner with the temporaries' reuse
+// setting, over the graph's nodes and edges; the users of a kernel's planes are the kernel and
+// every later dispatch that accesses a resource the kernel writes: its readers, which add the
+// planes themselves when the inferred graph defers the kernel's combine to them. (The graph's
+// may-alias edges from a kernel to later writers of other external buffers order those writers
+// after it, but they never read its planes.)
+static void planWorkspaces(ExecPlan &plan, const Graph &graph) {
+  constexpr std::size_t alignment = 256;
+  // Readers of what a kernel writes: later dispatches that access the same base resource.
+  auto readers = [&](std::size_t node) {
+    std::vector<planning::NodeId> out;
+    std::set<const Value *> written;
+    for (const BoundAccess &a : graph.nodes.at(node).accesses)
+      if (a.bits & Write) written.insert(getBaseResource(a.resource));
+    for (std::size_t n = node + 1; n < graph.nodes.size(); ++n) {
+      if (graph.nodes[n].kind != "dispatch") continue;
+      for (const BoundAccess &a : graph.nodes[n].accesses)
+        if (written.count(getBaseResource(a.resource))) { out.push_back(n); break; }
+    }
+    return out;
+  };
+  const int64_t heapId = int64_t(plan.heaps.size());
+  int64_t state = 0;
+  int device = -1;
+  std::vector<planning::Resource> planes;
+  std::vector<int64_t> owners;
+  for (const ExecKernel &k : plan.kernels) {
+    if (k.workspace < 0 || k.partials < -1) throw CompileError("library workspace sizes must be non-negative");
+    if (!k.workspace && k.partials <= 0) continue;
+    auto ordinal = deviceOrdinal(k.device);
+    if (!ordinal || (device >= 0 && *ordinal != device))
+      throw CompileError("library workspaces require one rocm:<ordinal> device");
+    device = *ordinal;
+    const std::string id = std::to_string(k.id);
+    if (k.workspace) {
+      plan.workspaces.push_back({"workspace" + id, "state", k.id, heapId, state, k.workspace});
+      state += int64_t(planning::alignUp(std::size_t(k.workspace), alignment));
+    }
+    if (k.partials > 0) {
+      std::vector<planning::NodeId> users{planning::NodeId(k.id)};
+      for (planning::NodeId s : readers(std::size_t(k.id))) users.push_back(s);
+      std::sort(users.begin(), users.end());
+      users.erase(std::unique(users.begin(), users.end()), users.end());
+      planes.push_back({"partials" + id, std::size_t(k.partials), alignment, "global", device,
+                        planning::ResourceKind::Temporary, std::move(users)});
+      owners.push_back(k.id);
+    }
+  }
+  if (device < 0) return;
+  int64_t bytes = state;
+  if (!planes.empty()) {
+    std::vector<planning::GraphEdge> edges;
+    for (const auto &[edge, _] : graph.edges) edges.push_back({edge.first, edge.second});
+    auto placed = planning::MemoryPlanner(graph.reuseStorage).tryPlan(graph.nodes.size(), edges, planes);
+    if (!placed) throw CompileError("library workspace planning failed: " + placed.error);
+    if (placed.value->heaps.size() != 1) throw CompileError("library workspace planes must form one heap");
+    for (const planning::Assignment &a : placed.value->assignments)
+      plan.workspaces.push_back({planes[a.resource].name, "partials", owners[a.resource], heapId,
+                                 state + int64_t(a.offset), int64_t(planes[a.resource].bytes)});
+    bytes = state + int64_t(placed.value->heaps.front().bytes);
+  }
+  plan.workspaceHeaps.push_back({heapId, bytes, int64_t(alignment), device, "global"});
 }
 
 ExecPlan lowerGraphToExec(const Module &module, const Op *function, const Graph &graph) {
@@ -1045,6 +1156,7 @@ ExecPlan lowerGraphToExec(const Module &module, const Op *function, const Graph 
     if (const Attr *shared = op->attr("ckl.hip.shared_memory")) k.sharedMemory = shared->i;
     if (const Attr *group = op->attr("ckl.hip.group")) k.group = group->s;
     if (const Attr *workspace = op->attr("ckl.hip.workspace")) k.workspace = workspace->i;
+    if (const Attr *partials = op->attr("ckl.hip.partials")) k.partials = partials->i;
 
     std::vector<Value *> actuals = dispatchArguments(op);
     for (size_t slot = 0; slot < actuals.size(); ++slot) {
@@ -1098,6 +1210,7 @@ ExecPlan lowerGraphToExec(const Module &module, const Op *function, const Graph 
     if (deps != reduced.end()) k.dependencies.assign(deps->second.begin(), deps->second.end());
     plan.kernels.push_back(std::move(k));
   }
+  planWorkspaces(plan, graph);
   plan.verify();
   return plan;
 }
@@ -1191,7 +1304,7 @@ std::string prepareHip(Module &module, const PrepareOptions &options) {
       dispatch->attrs["artifact"] = *art;
       dispatch->attrs["implementation"] = *impl;
       dispatch->attrs["ckl.hip.entry_point"] = *entry;
-      for (const char *key : {"grid", "block", "shared_memory", "constants", "group", "workspace"})
+      for (const char *key : {"grid", "block", "shared_memory", "constants", "group", "workspace", "partials"})
         if (const Attr *a = chosen->get(key)) dispatch->attrs[std::string("ckl.hip.") + key] = *a;
       if (const Attr *variants = chosen->get("variants")) {
         // Siblings: dispatches of this kernel in the same block whose first operand is the same
@@ -1214,7 +1327,7 @@ std::string prepareHip(Module &module, const PrepareOptions &options) {
         }
         if (best) {
           if (const Attr *e = best->get("entry_point")) dispatch->attrs["ckl.hip.entry_point"] = *e;
-          for (const char *key : {"grid", "block", "shared_memory", "constants", "workspace"})
+          for (const char *key : {"grid", "block", "shared_memory", "constants", "workspace", "partials"})
             if (const Attr *a = best->get(key)) dispatch->attrs[std::string("ckl.hip.") + key] = *a;
         }
       }

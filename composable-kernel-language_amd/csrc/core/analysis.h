@@ -98,6 +98,7 @@ struct Graph {
   std::string unavailableReason;
   planning::MemoryPlan plan;                                  // valid when planned
   std::vector<std::size_t> plannerToResource;                 // planner resource id -> resources index
+  bool reuseStorage = true;                                   // the storage-reuse setting of the plan
   std::string dot;
   std::string print() const;                                  // "ckl.graph" op text
 };
@@ -144,9 +145,20 @@ struct ExecKernel {
   std::vector<int64_t> logicalGrid, logicalBlock;
   int64_t sharedMemory = 0;
   std::string group;                  // sibling-grouping family ("" = none)
-  int64_t workspace = 0;              // private device workspace bytes of a library kernel
+  int64_t workspace = 0;              // library kernel: workspace state bytes (zero at every launch)
+  int64_t partials = -1;              // library kernel: split-reduction plane bytes (-1: no such pointer)
   std::vector<ExecArgument> arguments;
   std::vector<int64_t> dependencies;
+};
+
+// Device memory a library kernel uses beyond its arguments (HIP addition, no reference
+// counterpart), placed in the plan's workspace heap: role "state" (zero page and completion
+// counters, read as zero at every launch: never shared) or "partials" (split-reduction planes,
+// live from the kernel to its last reader: placed by the storage planner, so kernels whose
+// planes are never live together share memory).
+struct ExecWorkspace {
+  std::string name, role;
+  int64_t kernel = 0, heap = 0, offset = 0, bytes = 0;
 };
 
 struct ExecPlan {
@@ -154,6 +166,8 @@ struct ExecPlan {
   std::vector<Type> sourceArguments;
   std::vector<ExecHeap> heaps;
   std::vector<ExecResource> resources;
+  std::vector<ExecHeap> workspaceHeaps;   // at most one; its id follows the heaps' ids
+  std::vector<ExecWorkspace> workspaces;
   std::vector<ExecKernel> kernels;
   std::string print() const;          // "ckl_exec.plan" op text, one op per line
   void verify() const;                // throws CompileError

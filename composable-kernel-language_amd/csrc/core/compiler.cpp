@@ -62,6 +62,7 @@ void walkPlan(const ExecPlan &plan, const ArtifactLookup &artifacts, Sink &sink,
   };
   if (!plan.kernels.empty()) select(plan.kernels.front().artifact);
   for (const ExecHeap &h : plan.heaps) sink.heap(uint64_t(h.id), uint64_t(h.bytes));
+  for (const ExecHeap &h : plan.workspaceHeaps) sink.heap(uint64_t(h.id), uint64_t(h.bytes));
   std::map<std::string, uint64_t> resourceIds;
   for (size_t k = 0; k < plan.resources.size(); ++k) {
     const ExecResource &r = plan.resources[k];
@@ -72,6 +73,13 @@ void walkPlan(const ExecPlan &plan, const ArtifactLookup &artifacts, Sink &sink,
     } else {
       sink.resource(k, uint64_t(r.heap), uint64_t(r.offset), -1);
     }
+  }
+  // Library workspaces are heap placements like temporaries, numbered after the resources.
+  std::map<std::pair<int64_t, std::string>, uint64_t> workspaceIds;
+  for (const ExecWorkspace &w : plan.workspaces) {
+    const uint64_t id = plan.resources.size() + workspaceIds.size();
+    workspaceIds[{w.kernel, w.role}] = id;
+    sink.resource(id, uint64_t(w.heap), uint64_t(w.offset), -1);
   }
   for (const ExecKernel &k : plan.kernels) {
     select(k.artifact);
@@ -91,8 +99,23 @@ void walkPlan(const ExecPlan &plan, const ArtifactLookup &artifacts, Sink &sink,
         sink.argumentValue(a->bytes.data(), a->bytes.size(), "");
       }
     }
-    if (k.workspace < 0) throw CompileError("library workspace size must be non-negative");
-    if (k.workspace) sink.workspace(uint64_t(k.workspace));
+    if (k.workspace < 0 || k.partials < -1) throw CompileError("library workspace size must be non-negative");
+    // The workspace pointers follow the arguments: its state, then (kernels that take one) its
+    // partial planes, or a null pointer when it has none. A plan without a workspace heap gives
+    // the state as a private workspace (ckl_workspace).
+    auto state = workspaceIds.find({k.id, "state"});
+    if (state != workspaceIds.end()) sink.argumentResource(state->second, 0);
+    else if (k.workspace) sink.workspace(uint64_t(k.workspace));
+    if (k.partials >= 0) {
+      auto planes = workspaceIds.find({k.id, "partials"});
+      if (planes != workspaceIds.end()) {
+        sink.argumentResource(planes->second, 0);
+      } else {
+        if (k.partials) throw CompileError("kernel " + std::to_string(k.id) + " has partial planes but no placement");
+        const uint64_t null = 0;
+        sink.argumentValue(&null, sizeof null, "");
+      }
+    }
     for (int64_t d : k.dependencies) sink.dependency(uint64_t(d));
     sink.commit(uint64_t(k.id));
   }

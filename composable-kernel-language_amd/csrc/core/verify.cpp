@@ -12,7 +12,8 @@ const std::set<std::string> kCklOps = {
     "ckl.alloc", "ckl.free", "ckl.view", "ckl.subview", "ckl.load", "ckl.store", "ckl.load_element",
     "ckl.store_element", "ckl.atomic_rmw", "ckl.sync", "ckl.dispatch", "ckl.thread_id", "ckl.block_id",
     "ckl.block_dim", "ckl.grid_dim", "ckl.global_id", "ckl.graph", "ckl.graph_node", "ckl.graph_edge"};
-const std::set<std::string> kExecOps = {"ckl_exec.plan", "ckl_exec.heap", "ckl_exec.resource", "ckl_exec.kernel"};
+const std::set<std::string> kExecOps = {"ckl_exec.plan", "ckl_exec.heap", "ckl_exec.resource", "ckl_exec.kernel",
+                                         "ckl_exec.workspace_heap", "ckl_exec.workspace"};
 const std::set<std::string> kHostOps = {"ckl_host.entry", "ckl_host.call"};
 const std::set<std::string> kCallbacks = {"ckl_module", "ckl_heap", "ckl_resource", "ckl_kernel", "ckl_argument_resource",
                                           "ckl_argument_value", "ckl_workspace", "ckl_dependency", "ckl_commit"};
@@ -110,7 +111,9 @@ private:
     else if (n == "ckl.dispatch") dispatch(op);
     else if (n == "ckl.graph") graph(op);
     else if (n == "ckl.graph_node" || n == "ckl.graph_edge") parent(op, "ckl.graph");
-    else if (n == "ckl_exec.heap" || n == "ckl_exec.resource" || n == "ckl_exec.kernel") parent(op, "ckl_exec.plan");
+    else if (n == "ckl_exec.heap" || n == "ckl_exec.resource" || n == "ckl_exec.kernel" || n == "ckl_exec.workspace_heap" ||
+             n == "ckl_exec.workspace")
+      parent(op, "ckl_exec.plan");
     else if (n == "ckl_exec.plan") plan(op);
     else if (n == "ckl_host.entry") hostEntry(op);
     else if (n == "ckl_host.call") {
@@ -431,6 +434,24 @@ ExecPlan readPlan(const Module &module, const Op *op) {
         r.argument = std::stoll(r.name.substr(3));   // bound to host argument N, as the lowering names it
       }
       plan.resources.push_back(r);
+    } else if (c->name == "ckl_exec.workspace_heap") {
+      ExecHeap h;
+      h.id = required(c, "id", Attr::Int, "requires an id and positive byte size").i;
+      h.bytes = required(c, "bytes", Attr::Int, "requires an id and positive byte size").i;
+      h.alignment = required(c, "alignment", Attr::Int, "requires power-of-two alignment").i;
+      h.device = required(c, "device", Attr::Int, "requires a non-negative device ordinal").i;
+      if (h.device < 0) fail(c, "requires a non-negative device ordinal");
+      h.addressSpace = "global";
+      plan.workspaceHeaps.push_back(h);
+    } else if (c->name == "ckl_exec.workspace") {
+      ExecWorkspace w;
+      w.name = stringAttr(c, "name") ? *stringAttr(c, "name") : std::string();
+      w.role = stringAttr(c, "role") ? *stringAttr(c, "role") : std::string();
+      w.kernel = required(c, "kernel", Attr::Int, "requires kernel, heap, offset and bytes").i;
+      w.heap = required(c, "heap", Attr::Int, "requires kernel, heap, offset and bytes").i;
+      w.offset = required(c, "offset", Attr::Int, "requires kernel, heap, offset and bytes").i;
+      w.bytes = required(c, "bytes", Attr::Int, "requires kernel, heap, offset and bytes").i;
+      plan.workspaces.push_back(w);
     } else if (c->name == "ckl_exec.kernel") {
       ExecKernel k;
       k.id = required(c, "id", Attr::Int, "requires a non-negative id").i;
@@ -460,6 +481,7 @@ ExecPlan readPlan(const Module &module, const Op *op) {
       k.sharedMemory = *shared;
       if (const std::string *group = stringAttr(c, "group")) k.group = *group;
       if (auto workspace = intAttr(c, "workspace")) k.workspace = *workspace;
+      if (auto partials = intAttr(c, "partials")) k.partials = *partials;
       const Attr *dependencies = c->attr("dependencies");
       if (!dependencies || dependencies->kind != Attr::DenseI64) fail(c, "requires a dependencies array");
       k.dependencies = dependencies->dense;

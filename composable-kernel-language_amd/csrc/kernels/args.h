@@ -36,19 +36,22 @@ struct CKL_ALIGN RmsStatsArgs { const float *x; float *inv; float eps; int B, C;
 // dst[b, c] = x[b, c] * inv[b] * gain[layer, c]   (workloads.py:52-58)
 struct CKL_ALIGN RmsApplyArgs { const float *x; const float *inv; const float *gain; float *dst; int B, C, layer; };
 // dst[b, o] = sum_i x[b, i] * w[layer, i, o]   (workloads.py:61-69)
-// With kSplit > 1 the reduction is split over workgroups that leave partial planes in the
-// workspace; `deferred` = 0: the last workgroup of a tile adds them into dst; 1 (set by the
+// With kSplit > 1 the reduction is split over workgroups that leave partial planes in
+// `partials`; `deferred` = 0: the last workgroup of a tile adds them into dst; 1 (set by the
 // executor, see PartialSource): dst is not written and the consumer adds the planes.
 struct CKL_ALIGN LinearArgs {
   const float *x; const float *w; float *dst; int B, I, O, layer;
   int tilesN, kSplit, kChunk, deferred;
   unsigned char *workspace;
+  float *partials;
 };
 
-// Workspace layout of the linear family: kLinearZeroPage bytes that stay zero (padding loads read
-// them), the split completion counters (uint32 per output tile, padded to 256 B), then the
-// partial planes float[kSplit][rows][O], rows = B for the vector path (ckl_linear_rowvec) and
-// 32 * ceil(B / 32) for the MFMA paths.
+// Workspace of the linear family, two ranges of the plan's workspace heap. `workspace` (state,
+// reads zero at every launch, never shared): kLinearZeroPage bytes that stay zero (padding loads
+// read them), then the split completion counters (uint32 per output tile, padded to 256 B; reset
+// by the last workgroup of each tile). `partials` (null when kSplit = 1): the partial planes
+// float[kSplit][rows][O], rows = B for the vector path (ckl_linear_rowvec) and 32 * ceil(B / 32)
+// for the MFMA paths, live from the launch until the readers of dst have run.
 constexpr int kLinearZeroPage = 256;
 // The MFMA linear's epilogue hands the accumulators of EM members through LDS in one pass:
 // 16 KB per member and weight column of a lane (4 waves x 16 registers x 64 lanes x 4 bytes), at
@@ -59,9 +62,6 @@ constexpr int linearEpilogueMembers(int M, int J) {
 }
 constexpr uint64_t linearCounterBytes(uint64_t counters) { return (counters * 4 + 255) & ~uint64_t(255); }
 constexpr uint64_t linearPlaneRows(int B, bool vector) { return vector ? uint64_t(B) : uint64_t((B + 31) / 32) * 32; }
-constexpr uint64_t linearPartialsOffset(int B, int tilesN, bool vector) {
-  return kLinearZeroPage + linearCounterBytes(uint64_t(vector ? B : (B + 31) / 32) * uint64_t(tilesN));
-}
 
 // A consumer operand that is the sum of a split linear's partial planes (the linear's combine
 // deferred to its consumer): value[i] = sum over g < parts of partials[g * planeStride + i], added

@@ -524,24 +524,23 @@ CKL_ENTRY(embedding__rms_stats__rms_apply, EmbeddingRmsChainArgs, embedding__rms
 // tile's completion counter; the last one to arrive adds the kSplit partials in kg order,
 // writes dst and resets the counter, so the result is deterministic and replays need no reset.
 //
-// workspace layout: counters (rowTiles*tilesN uint32, padded to 256 B), then partial tiles
-// float[kSplit][rowTiles*rowsPerTile][O] (rowsPerTile = 32 for MFMA, B for the vector path).
+// workspace: the zero page, then counters (rowTiles*tilesN uint32, padded to 256 B); partials:
+// partial tiles float[kSplit][rowTiles*rowsPerTile][O] (rowsPerTile = 32 for MFMA, B for the
+// vector path).
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 // s_waitcnt immediate (gfx9 encoding) that waits for vmcnt == 0 only: outstanding vector memory
 // operations of the wave, stores included, have completed.
 constexpr int kWaitStores = 0x0F70;
 
-// Workspace layout of the linear family (args.h): kLinearZeroPage bytes that stay zero (loads of
+// Workspace of the linear family (args.h): kLinearZeroPage bytes that stay zero (loads of
 // padding read here, so they need neither a predicate nor a select on the loaded value), then the
-// split completion counters, then the partial planes.
+// split completion counters; the partial planes have their own pointer.
 constexpr int kZeroPage = kLinearZeroPage;
 __device__ __forceinline__ unsigned *split_counters(const LinearArgs &a) {
   return reinterpret_cast<unsigned *>(a.workspace + kZeroPage);
 }
-__device__ __forceinline__ float *split_partials(const LinearArgs &a, bool vector) {
-  return reinterpret_cast<float *>(a.workspace + linearPartialsOffset(a.B, a.tilesN, vector));
-}
+__device__ __forceinline__ float *split_partials(const LinearArgs &a, bool) { return a.partials; }
 
 // Cross-workgroup partial tiles live in the workspace and are written and read only with
 // agent-scope atomic stores/loads (sc1: coherent across the MI355X's per-XCD L2 caches without
@@ -1015,26 +1014,18 @@ __device__ __forceinline__ float score_scalar(const float *q, const float *key, 
 }
 // Vector layout of the scores: groups of G lanes hold one cache row, each lane P float4 pieces of
 // it (pieces part + G*j, j < P): P = 1 and G = D/4 for D <= 32, P = 2 for D <= 64, else P = 4,
-// with G = D/(4P) a power of two (8 lanes for D = 64 and 128, 16 for D = 256); other D take the
-// sequential dot product. Each lane adds its 4P products with explicit FMAs in piece order, then
+// with G = D/(4P) a power of two (8 lanes for D = 64 and 128, 16 for D = 256); other D (D = 96:
+// G = 6) take the sequential dot product. A P = 3 instantiation for D = 96 would give it 8-lane
+// groups, but it doubled the VGPRs of the rope/attention chain kernel for every D (69 -> 148,
+// with scratch), so the chain ran 40% slower at D = 128; it is not instantiated. Each lane adds its 4P products with explicit FMAs in piece order, then
 // the row is summed over its G lanes (group_sum), so with 8-lane groups a row costs three DPP
 // steps instead of a 32-lane butterfly. A wave load covers 64/G rows; a lane keeps kScoreBatch
 // pieces in flight (kScoreBatch/P rows).
-__device__ __forceinline__ bool score_groups(int D, int P) {   // G = D/(4P) lanes a row: a power of two
-  const int G = D / (4 * P);
-  return G > 0 && G * 4 * P == D && (G & (G - 1)) == 0;
-}
-// P = 1, 2, 4 for D <= 32, <= 64, larger (8-lane groups for D = 64 and 128); a D those leave
-// without power-of-two groups takes the smallest P that gives them (D = 96: P = 3, 8 lanes).
-__device__ __forceinline__ int score_pieces(int D) {
-  const int preferred = D <= 32 ? 1 : D <= 64 ? 2 : 4;
-  if (score_groups(D, preferred)) return preferred;
-  for (int P = 1; P <= 4; ++P)
-    if (score_groups(D, P)) return P;
-  return preferred;
-}
+__device__ __forceinline__ int score_pieces(int D) { return D <= 32 ? 1 : D <= 64 ? 2 : 4; }
 __device__ __forceinline__ bool scores_vector_layout(int D) {
-  return !(D & 3) && D <= 256 && score_groups(D, score_pieces(D));
+  if ((D & 3) || D > 256) return false;
+  const int P = score_pieces(D), G = D / (4 * P);
+  return G * 4 * P == D && (G & (G - 1)) == 0;        // G lanes a row: a power of two
 }
 // Partial dot product of a lane's P pieces of q and of one key row.
 template <int P> __device__ __forceinline__ float dot_pieces(const float4 (&q)[P], const float4 *k) {
@@ -1106,7 +1097,6 @@ template <bool NT> __device__ void attention_scores_body(const ScoresArgs &a, in
     switch (score_pieces(a.D)) {
       case 1: attention_scores_rows<NT, 1>(a, q, keys, scores, w0, w1); break;
       case 2: attention_scores_rows<NT, 2>(a, q, keys, scores, w0, w1); break;
-      case 3: attention_scores_rows<NT, 3>(a, q, keys, scores, w0, w1); break;
       default: attention_scores_rows<NT, 4>(a, q, keys, scores, w0, w1); break;
     }
   } else {
@@ -1420,7 +1410,6 @@ __device__ void attention_scores__softmax__attention_values_body(const Attention
   switch (score_pieces(a.scores.D)) {
     case 1: attention_chain_row<NT, 1>(a.scores, a.softmax, a.values, bh, q, p, rowScores, none, false); break;
     case 2: attention_chain_row<NT, 2>(a.scores, a.softmax, a.values, bh, q, p, rowScores, none, false); break;
-    case 3: attention_chain_row<NT, 3>(a.scores, a.softmax, a.values, bh, q, p, rowScores, none, false); break;
     default: attention_chain_row<NT, 4>(a.scores, a.softmax, a.values, bh, q, p, rowScores, none, false); break;
   }
 }
@@ -1490,7 +1479,6 @@ template <bool NT> __device__ void rope_attention_stream(const RopeAttentionChai
   switch (score_pieces(a.scores.D)) {
     case 1: rope_attention_rows<NT, 1>(a, block); break;
     case 2: rope_attention_rows<NT, 2>(a, block); break;
-    case 3: rope_attention_rows<NT, 3>(a, block); break;
     default: rope_attention_rows<NT, 4>(a, block); break;
   }
 }

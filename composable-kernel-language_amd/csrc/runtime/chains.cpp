@@ -970,8 +970,8 @@ std::map<size_t, Launch> deferCombines(const Plan &plan, const std::vector<bool>
     const bool vector = l.name == "ckl_linear_rowvec";
     const uint64_t stride = linearPlaneRows(a.B, vector) * uint64_t(a.O);
     if (!all || stride % 4) continue;
-    PartialSource source{reinterpret_cast<const float *>(a.workspace + linearPartialsOffset(a.B, a.tilesN, vector)),
-                         int64_t(stride), a.kSplit, 0};
+    if (!a.partials) continue;
+    PartialSource source{a.partials, int64_t(stride), a.kSplit, 0};
     for (const Operand &o : found->second) {
       std::vector<uint8_t> &bytes = chains[o.chain].launch.arguments;
       if (o.source + sizeof source > bytes.size()) throw std::logic_error("chain block has no room for a partial source");

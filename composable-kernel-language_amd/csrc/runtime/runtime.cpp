@@ -485,6 +485,30 @@ Invocation::~Invocation() {
   }
 }
 
+void Invocation::placeHeaps() {
+  if (pendingHeaps.empty()) return;
+  uint64_t total = 0;
+  std::vector<uint64_t> offsets;
+  for (const auto &[id, bytes] : pendingHeaps) {
+    offsets.push_back(total);
+    total += (bytes + 255) & ~uint64_t(255);
+  }
+  device->makeCurrent();
+  std::shared_ptr<Buffer> arena;
+  if (staticArena) {
+    arena = importBuffer(device, carve(total), total);
+  } else {
+    arena = allocateBuffer(device, total);
+    ++allocations;
+  }
+  // Library workspaces keep state that must read zero (zero pages, completion counters); the
+  // whole range is cleared once, before any launch of this invocation.
+  staticScratchClear(arena->address(), total, stream);
+  for (size_t k = 0; k < pendingHeaps.size(); ++k)
+    heaps[pendingHeaps[k].first] = sliceBuffer(arena, offsets[k], pendingHeaps[k].second);
+  pendingHeaps.clear();
+}
+
 uint64_t Invocation::carve(uint64_t bytes) {
   const uint64_t start = (arenaUsed + 255) & ~uint64_t(255);
   if (!bytes || start > arenaLimit || bytes > arenaLimit - start) {
@@ -988,6 +1012,8 @@ static std::shared_ptr<Invocation> bindWith(const std::shared_ptr<ProgramState> 
   void *entryArguments[] = {&frame, &values, program->entryContext};
   program->entry(entryArguments);
   invocation->bindingAddresses = nullptr;
+  // Heaps no resource asked for are placed as well (the binding's memory is its plan's).
+  callback(invocation.get(), [](Invocation &f) { f.placeHeaps(); });
   if (!invocation->error.empty()) {
     // The reference reports callback failures as runtime errors; a program too large for the
     // static arena is the caller's argument error.
@@ -1013,17 +1039,21 @@ extern "C" void ckl_module(void *frame, const char *identity, const void *binary
   });
 }
 
+// Heaps are recorded and placed together, in one allocation (or one range of the static arena)
+// cleared by one fill kernel, when the entry first needs an address (ckl::rt::placeHeaps).
 extern "C" void ckl_heap(void *frame, uint64_t id, uint64_t bytes) {
   ckl::rt::callback(frame, [&](Invocation &f) {
+    if (!bytes) throw std::invalid_argument("heaps must be non-empty");
     if (f.heaps.size() <= id) f.heaps.resize(id + 1);
-    f.heaps[id] = f.staticArena ? ckl::rt::importBuffer(f.device, f.carve(bytes), bytes)
-                                : ckl::rt::allocateBuffer(f.device, bytes);
-    if (!f.staticArena) ++f.allocations;
+    if (f.heaps[id] || std::any_of(f.pendingHeaps.begin(), f.pendingHeaps.end(), [&](auto &h) { return h.first == id; }))
+      throw std::invalid_argument("heap " + std::to_string(id) + " declared twice");
+    f.pendingHeaps.push_back({id, bytes});
   });
 }
 
 extern "C" void ckl_resource(void *frame, uint64_t id, uint64_t heap, uint64_t offset, void *external) {
   ckl::rt::callback(frame, [&](Invocation &f) {
+    f.placeHeaps();
     if (f.resources.size() <= id) f.resources.resize(id + 1);
     if (f.temporaryResources.size() <= id) f.temporaryResources.resize(id + 1, false);
     if (f.resourceArgument.size() <= id) f.resourceArgument.resize(id + 1, -1);

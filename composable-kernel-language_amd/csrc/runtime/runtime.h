@@ -180,6 +180,10 @@ struct Invocation {
   bool ownsStream = true;
   bool arenaExceeded = false;                       // the static arena was too small (bind fails)
   uint64_t carve(uint64_t bytes);                   // 256-aligned arena range for `bytes`
+  // Heaps declared (ckl_heap) and not yet placed: {id, bytes}. placeHeaps() puts all of them in
+  // one allocation (or one static-arena range), cleared by one fill kernel on `stream`.
+  std::vector<std::pair<uint64_t, uint64_t>> pendingHeaps;
+  void placeHeaps();
 
   // The program arguments as bound: buffer addresses and scalar bytes; for each plan resource the
   // program argument it is (-1: a heap placement); the program that was asked for (the bound one

@@ -47,7 +47,12 @@ class Launch:
     block: int = BLOCK
     shared: int = 0
     entry: str = ""          # entry point when the family has several (default ckl_<name>)
-    workspace: int = 0       # private zero-initialised device workspace bytes (ckl_workspace)
+    # Device workspace the compiled plan gives the kernel: `workspace` bytes of state that reads
+    # zero at every launch (zero page, completion counters), and, when `partials` >= 0, a second
+    # pointer to `partials` bytes of split-reduction planes (0: a null pointer) that live only
+    # until the kernel's readers have run, so the plan may share them between kernels.
+    workspace: int = 0
+    partials: int = -1
     # (members, Launch): the launch a dispatch takes instead when at least `members` dispatches
     # of the kernel in its block multiply the same first operand (siblings the inferred graph
     # runs as one shared-operand launch); the native prepare step picks it per dispatch, so every
@@ -149,12 +154,13 @@ def linear_tiling(b: int, i: int, o: int, members: int = 1) -> dict:
         block = 64 * waves
     else:
         return None
-    workspace = LINEAR_ZERO_PAGE
+    workspace, partials = LINEAR_ZERO_PAGE, 0
     if split > 1:
         counters = row_tiles * tiles if entry != "ckl_linear_rowvec" else b * tiles
-        workspace += _cdiv(4 * counters, 256) * 256 + 4 * split * rows * o
+        workspace += _cdiv(4 * counters, 256) * 256
+        partials = 4 * split * rows * o
     return dict(grid=row_tiles * split * tiles, tiles=tiles, split=split, chunk=chunk, shared=shared, entry=entry,
-                workspace=workspace, block=block)
+                workspace=workspace, partials=partials, block=block)
 
 
 def _linear(shapes, consts, ext):
@@ -164,7 +170,8 @@ def _linear(shapes, consts, ext):
         return None
     def launch(t, variants=()):
         return Launch(t["grid"], (b, i, o, layer, t["tiles"], t["split"], t["chunk"], 0), block=t["block"],
-                      shared=t["shared"], entry=t["entry"], workspace=t["workspace"], variants=variants)
+                      shared=t["shared"], entry=t["entry"], workspace=t["workspace"], partials=t["partials"],
+                      variants=variants)
 
     t = linear_tiling(b, i, o)
     if t is None:
@@ -349,6 +356,8 @@ def selection_attribute(selections: dict, artifact: str) -> str:
                   f'implementation = "ckl.hip.library.{s.kernel.name}"', f"shared_memory = {s.launch.shared} : i64"]
         if s.launch.workspace:
             fields.append(f"workspace = {s.launch.workspace} : i64")
+        if s.launch.partials >= 0:
+            fields.append(f"partials = {s.launch.partials} : i64")
         if s.launch.variants:
             variants = []
             for members, v in s.launch.variants:
@@ -356,7 +365,7 @@ def selection_attribute(selections: dict, artifact: str) -> str:
                            "constants = [" + ", ".join(f"{int(c)} : i32" for c in v.constants) + "]",
                            f'entry_point = "{v.entry or s.kernel.entry_point}"', f"grid = array<i64: {v.grid}, 1, 1>",
                            f"members = {members} : i64", f"shared_memory = {v.shared} : i64",
-                           f"workspace = {v.workspace} : i64"]
+                           f"workspace = {v.workspace} : i64", f"partials = {v.partials} : i64"]
                 variants.append("{" + ", ".join(variant) + "}")
             fields.append("variants = [" + ", ".join(variants) + "]")
         if s.kernel.groupable:

@@ -185,8 +185,10 @@ int ckl_invocation_rebind(ckl_invocation *invocation, const ckl_argument *argume
 /* Graph executables this invocation has instantiated so far (modes 1-4). */
 int ckl_invocation_graph_instantiations(ckl_invocation *invocation, uint64_t *count);
 /* Device memory of the binding (no reference counterpart; the reference reports heap bytes from
- * the plan text): out[0] planned heap bytes, out[1] library-kernel workspace bytes, out[2] device
- * allocations the bind made (0 for ckl_bind_static). */
+ * the plan text): out[0] bytes of the heaps the entry declared (ckl_heap: the plan's temporaries
+ * and its library-workspace heap), placed together in one allocation cleared once at bind;
+ * out[1] bytes of private workspaces (ckl_workspace); out[2] device allocations the bind made
+ * (0 for ckl_bind_static). */
 int ckl_invocation_memory(ckl_invocation *invocation, uint64_t out[3]);
 /* Independent requests (replaces the thread-pool burst of benchmarks/decoder/experiment.py:53-70,
  * one native benchmark call per request thread): `iterations` runs of `batch` steps of each of
@@ -251,9 +253,13 @@ void ckl_dependency(void *frame, uint64_t id);
 void ckl_commit(void *frame, uint64_t id);
 /* HIP addition (no reference counterpart): gives the pending kernel a private device workspace of
  * `bytes` bytes, zero-filled once at bind and owned by the invocation, and appends its address
- * as the next kernel argument. Library kernels that combine partial results across workgroups
- * (split reductions with self-resetting completion counters) use it; the reference's kernels
- * never need one. */
+ * as the next kernel argument. Compiled plans place their library kernels' workspaces in a
+ * planned workspace heap instead (a ckl_heap after the temporaries' heaps, its placements
+ * declared with ckl_resource and passed with ckl_argument_resource); this callback serves host
+ * entries written by hand and plans without a workspace heap.
+ * Every ckl_heap of one bind is placed in a single device allocation (ckl_bind_static: one range
+ * of the static arena) when the entry first declares a resource, and that range is zero-filled
+ * once, by one kernel on the invocation's stream. */
 void ckl_workspace(void *frame, uint64_t bytes);
 
 #ifdef __cplusplus

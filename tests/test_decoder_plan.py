@@ -136,3 +136,65 @@ def test_sibling_linears_take_their_shared_tiling():
     for t, n in ((siblings, 3 * c.layers), (single, c.layers), (gate_up, 2 * c.layers), (down, c.layers), (head, 1)):
         expected[(t["entry"], t["grid"])] = expected.get((t["entry"], t["grid"]), 0) + n
     assert launches == expected
+
+
+def workspace_plan(ir):
+    """(kernels: id -> (dependencies, resource names of its arguments), placements)."""
+    kernels = {}
+    for line in ir.splitlines():
+        if '"ckl_exec.kernel"' not in line:
+            continue
+        node = int(re.search(r"\bid = (\d+)", line).group(1))
+        match = re.search(r"dependencies = array<i64(?:: ([\d, ]+))?>", line).group(1)
+        deps = [int(v) for v in match.split(",")] if match else []
+        kernels[node] = (deps, re.findall(r'resource = "([^"]+)"', line))
+    placements = [dict(kernel=int(m.group(3)), name=m.group(4), offset=int(m.group(5)), bytes=int(m.group(1)),
+                       role=m.group(6))
+                  for m in re.finditer(r'"ckl_exec.workspace"\(\) <\{bytes = (\d+) : i64, heap = (\d+) : i64, '
+                                       r'kernel = (\d+) : i64, name = "(\w+)", offset = (\d+) : i64, role = "(\w+)"', ir)]
+    return kernels, placements
+
+
+@pytest.mark.parametrize("name", ["small", "deep", "large"])
+def test_library_workspaces_share_memory_only_between_ordered_lifetimes(name):
+    """The workspace heap of the plan (library kernels' state and partial planes, planned apart
+    from the temporaries): with storage reuse off nothing overlaps; with it on, two placements
+    overlap only if both are partial planes and every reader of the first kernel's outputs
+    (kernels taking a resource it writes, from the dependency graph's access list) precedes the
+    second kernel in the plan's dependency
+    order, so no launch order the dependencies allow can see one kernel's planes overwritten
+    while they are still read. Reuse shrinks the large decoder's workspaces to a few layers'
+    worth of planes."""
+    lowered = decode.lower(signature=signature(CONFIGS[name]))
+    graph = lowered.analyze("prepare-hip", "build-graph")
+    written = {}
+    for node in re.finditer(r'"ckl.graph_node"\(\) <\{accesses = \[(.*?)\], id = (\d+) : i64', graph):
+        written[int(node.group(2))] = set(re.findall(r'effects = \[[^\]]*"write"[^\]]*\], region = "\w+", '
+                                                     r'resource = "([^"]+)"', node.group(1)))
+    sizes = {}
+    for reuse in (False, True):
+        ir = lowered.compile(fuse_pointwise=False, reuse_storage=reuse).executable_ir
+        kernels, placements = workspace_plan(ir)
+        heap = [int(m) for m in re.findall(r'"ckl_exec.workspace_heap"\(\) <\{alignment = 256 : i64, bytes = (\d+)', ir)]
+        assert len(heap) == 1 and all(p["offset"] + p["bytes"] <= heap[0] for p in placements)
+        sizes[reuse] = heap[0]
+        reach = {}
+        for node in sorted(kernels):
+            reach[node] = set(kernels[node][0])
+            for d in kernels[node][0]:
+                reach[node] |= reach[d]
+        for a in placements:
+            for b in placements:
+                if a is b or a["offset"] >= b["offset"] + b["bytes"] or b["offset"] >= a["offset"] + a["bytes"]:
+                    continue
+                assert reuse and a["role"] == b["role"] == "partials", (a, b)
+                first, second = sorted((a["kernel"], b["kernel"]))
+                outputs = written[first]
+                assert outputs
+                readers = [k for k in kernels if k > first and outputs & set(kernels[k][1])]
+                assert all(r in reach[second] for r in [first] + readers), (first, second)
+        if not reuse:
+            assert sum(p["bytes"] for p in placements) <= heap[0]
+    assert sizes[True] <= sizes[False]
+    if name == "large":
+        assert sizes[False] > 50 << 20 and sizes[True] < 10 << 20
