@@ -204,6 +204,8 @@ def run_config(name, c, args, device, checker):
     t0 = time.time()
     arrays, prompts = synthetic_inputs(c, args.seed, init="baseline")
     session = DecoderSession(c, device, arrays=arrays)
+    bind_allocations = {"reuse_off": session.invocations[False].bind_allocations,
+                        "reuse_on": session.invocations[True].bind_allocations}
     t1 = time.time()
     session.prefill(prompts, mode="ordinary", progress=lambda done, total: log(f"[{name}] prefill {done}/{total}"))
     t2 = time.time()
@@ -212,6 +214,8 @@ def run_config(name, c, args, device, checker):
     expected = checker.expected(name, session, sorted(counts))
     log(f"[{name}] expected states for {sorted(counts)} steps from the NumPy checker in {time.time() - t2:.1f}s")
     table = time_variants(session, c, args.steps, args.warmup, expected, f"[{name}]", args.variants)
+    # Temporaries the inferred graph moved out of storage the plan shares (decided at its first build).
+    moved = {"reuse_off": session.invocations[False].private_bytes, "reuse_on": session.invocations[True].private_bytes}
     heap = {str(reuse): heap_bytes(program) for reuse, program in session.programs.items()}
 
     def median(variant):
@@ -239,8 +243,8 @@ def run_config(name, c, args, device, checker):
                   scratch_bytes={"reuse_off": heap["False"], "reuse_on": heap["True"]},
                   workspace_bytes={"reuse_off": heap_bytes(session.programs[False], '"ckl_exec.workspace_heap"'),
                                    "reuse_on": heap_bytes(session.programs[True], '"ckl_exec.workspace_heap"')},
-                  bind_allocations={"reuse_off": session.invocations[False].bind_allocations,
-                                    "reuse_on": session.invocations[True].bind_allocations},
+                  bind_allocations=bind_allocations,
+                  moved_temporary_bytes=moved,
                   tokens_per_s=c.batch * 1e6 / step_us,
                   algorithmic_bytes_per_step=mean_bytes,
                   step_hbm_fraction=mean_bytes / (step_us * 1e-6) / HBM_PEAK,
@@ -713,7 +717,7 @@ def summary_line(name, r):
     """The few figures of a non-headline configuration that the stdout line carries."""
     keep = ("inferred_us", "capture_us", "branches_us", "contracted_us", "stream_us", "ordinary_us",
             "inferred_reuse_us", "inferred_over_capture", "branches_over_capture", "scratch_bytes", "workspace_bytes",
-            "step_hbm_fraction", "logits_normwise", "runs_verified")
+            "moved_temporary_bytes", "step_hbm_fraction", "logits_normwise", "runs_verified")
     out = {k: r[k] for k in keep}
     if "cpu_baseline" in r:
         out["cpu_us"] = r["cpu_baseline"]["value"]
@@ -818,7 +822,8 @@ def measure(args, checker):
                                            "stream_us", "inferred_reuse_us", "batched_inferred_us",
                                            "inferred_over_capture", "branches_over_capture",
                                            "contracted_over_capture", "stream_over_capture", "scratch_bytes",
-                                           "workspace_bytes", "bind_allocations", "tokens_per_s", "step_hbm_fraction",
+                                           "workspace_bytes", "bind_allocations", "moved_temporary_bytes",
+                                           "tokens_per_s", "step_hbm_fraction",
                                            "logits_normwise", "runs_verified")},
                    "verification": "every run of every variant against the NumPy decoder (oracle/decoder.py) from "
                                    "the GPU-prefilled state: tokens, history, position exact; logits atol 2e-5 rtol "

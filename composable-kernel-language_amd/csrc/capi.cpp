@@ -104,6 +104,8 @@ std::shared_ptr<ckl::rt::ProgramState> stateFor(const std::shared_ptr<ckl::Compi
   state->entryContext = compiled.get();
   state->bufferBytes = compiled->bufferBytes;
   state->scalarTypes = compiled->scalarTypes;
+  for (const ckl::ExecResource &r : compiled->plan.resources)
+    state->resourceBytes.push_back(r.kind == "temporary" ? uint64_t(r.bytes) : 0);
   state->owner = compiled;
   if (compiled->fallback) state->aliasFallback = stateFor(compiled->fallback);
   return state;

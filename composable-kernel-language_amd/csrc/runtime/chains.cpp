@@ -783,7 +783,8 @@ void trace(size_t head, const Rule &rule, const char *outcome) {
 
 } // namespace
 
-std::vector<Chain> findChains(const Plan &plan, const std::vector<bool> &temporary) {
+std::vector<Chain> findChains(const Plan &plan, const std::vector<bool> &temporary,
+                              std::vector<std::vector<size_t>> *refused) {
   const size_t n = plan.nodes.size();
   std::vector<std::vector<size_t>> successors(n);
   for (size_t k = 0; k < n; ++k) for (size_t d : plan.nodes[k].dependencies) successors[d].push_back(k);
@@ -878,6 +879,7 @@ std::vector<Chain> findChains(const Plan &plan, const std::vector<bool> &tempora
       fused.groupFunction = group;
       if (const char *why = rule.build(launches, internal, fused)) {
         trace(head, rule, why);
+        if (refused && why == kOverlap) refused->push_back(members);
         continue;
       }
       std::vector<size_t> trial = unit;

@@ -4,8 +4,10 @@
 
 #include <algorithm>
 #include <chrono>
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <set>
 #include <stdexcept>
 
 namespace ckl::rt {
@@ -547,6 +549,12 @@ std::vector<Unit> Invocation::buildUnits(int mode, uint64_t batch, const Plan &r
     for (size_t k = 0; k < repeated.nodes.size(); ++k) units.push_back({{k}, repeated.nodes[k].launch});
     return units;
   }
+  if (!relocationDecided) {
+    relocationDecided = true;
+    relocateForChains();
+    if (batch == 1) return buildUnits(mode, batch, plan);      // the repeated plan predates the move
+    return buildUnits(mode, batch, plan.repeat(batch));
+  }
   std::vector<Chain> chains = findChains(plan, temporaryResources);
   std::map<size_t, Launch> deferred = deferCombines(plan, temporaryResources, chains);
   units = groupPlan(repeated, chains, deferred, batch);
@@ -857,7 +865,101 @@ std::array<uint64_t, 3> Invocation::memory() const {
   for (const auto &h : heaps)
     if (h) out[0] += h->bytes;
   for (const auto &w : workspaces) out[1] += w->bytes;
+  if (relocation) out[1] += relocation->bytes;
   return out;
+}
+
+// Storage reuse may put a dispatch's output where an input of the dispatch before it lived: dead
+// in dispatch order, but live inside a chain that runs both dispatches as one launch, whose
+// workgroups would then overwrite input rows other workgroups have not read yet. For the chains
+// refused for that reason, the temporary of each overlapping pair that the plan uses later (the
+// one placed into the other's dead storage) moves to a separate allocation of this invocation,
+// provided a trial with the moved addresses shows more chains are then taken. Temporaries hold
+// nothing from one execution to the next, so every run mode may use the moved addresses; the
+// plan's heaps and offsets are unchanged. Static bindings allocate nothing and keep the plan.
+void Invocation::relocateForChains() {
+  const std::vector<uint64_t> &bytes = program->resourceBytes;
+  if (staticArena || bytes.empty()) return;
+  // Dispatches a set of chains saves (each chain runs its members as one launch).
+  auto saved = [](const std::vector<Chain> &chains) {
+    size_t out = 0;
+    for (const Chain &c : chains) out += c.members.size() - 1;
+    return out;
+  };
+  std::vector<std::vector<size_t>> refused;
+  const size_t before = saved(findChains(plan, temporaryResources, &refused));
+  if (refused.empty()) return;
+  std::vector<size_t> first(resources.size(), plan.nodes.size());    // first plan node using each resource
+  for (size_t k = plan.nodes.size(); k-- > 0;)
+    for (int64_t id : plan.nodes[k].launch.slotResources)
+      if (id >= 0 && size_t(id) < first.size()) first[size_t(id)] = k;
+  auto movable = [&](int64_t id) {
+    return id >= 0 && size_t(id) < bytes.size() && size_t(id) < temporaryResources.size() &&
+           temporaryResources[size_t(id)] && bytes[size_t(id)] > 0;
+  };
+  std::set<int64_t> moved;
+  for (const std::vector<size_t> &members : refused) {
+    std::set<int64_t> ids;
+    for (size_t m : members)
+      for (int64_t id : plan.nodes[m].launch.slotResources)
+        if (movable(id)) ids.insert(id);
+    for (int64_t a : ids)
+      for (int64_t b : ids) {
+        if (a >= b || first[size_t(a)] == first[size_t(b)]) continue;
+        const uint64_t a0 = resources[size_t(a)], b0 = resources[size_t(b)];
+        if (a0 + bytes[size_t(a)] <= b0 || b0 + bytes[size_t(b)] <= a0) continue;
+        moved.insert(first[size_t(a)] > first[size_t(b)] ? a : b);
+      }
+  }
+  // The plan with `set` moved to consecutive 256-byte-aligned ranges from `base`.
+  auto movedTo = [&](const std::set<int64_t> &set, uint64_t base, std::map<int64_t, uint64_t> *offsets) {
+    std::map<int64_t, uint64_t> offset;
+    uint64_t total = 0;
+    for (int64_t id : set) {
+      offset[id] = total;
+      total += (bytes[size_t(id)] + 255) & ~uint64_t(255);
+    }
+    Plan out = plan;
+    for (PlanNode &node : out.nodes) {
+      Launch &l = node.launch;
+      for (size_t s = 0; s < l.slotResources.size(); ++s) {
+        auto it = offset.find(l.slotResources[s]);
+        if (it == offset.end()) continue;
+        if (l.slotSizes[s] != 8) throw std::logic_error("an address slot is not 8 bytes");
+        uint64_t value;
+        std::memcpy(&value, l.arguments.data() + l.slotOffsets[s], 8);
+        value = value - resources[size_t(it->first)] + base + it->second;
+        std::memcpy(l.arguments.data() + l.slotOffsets[s], &value, 8);
+      }
+    }
+    if (offsets) *offsets = std::move(offset);
+    return out;
+  };
+  // Trials only compare addresses: a base above every device address cannot overlap a buffer.
+  const uint64_t trialBase = uint64_t(1) << 56;
+  auto gain = [&](const std::set<int64_t> &set) { return saved(findChains(movedTo(set, trialBase, nullptr), temporaryResources)); };
+  const size_t best = moved.empty() ? before : gain(moved);
+  if (best <= before) return;
+  // Keep only what the gain needs: drop each temporary whose move does not contribute.
+  for (auto it = moved.begin(); it != moved.end();) {
+    std::set<int64_t> fewer = moved;
+    fewer.erase(*it);
+    if (gain(fewer) >= best) it = moved.erase(it);
+    else ++it;
+  }
+  std::map<int64_t, uint64_t> offset;
+  uint64_t total = 0;
+  for (int64_t id : moved) total += (bytes[size_t(id)] + 255) & ~uint64_t(255);
+  if (const char *v = std::getenv("CKL_CHAIN_TRACE"); v && std::strcmp(v, "1") == 0) {
+    std::fprintf(stderr, "[ckl chains] %zu chains refused for overlap; moving %zu temporaries (%llu bytes):", refused.size(),
+                 moved.size(), (unsigned long long)total);
+    for (int64_t id : moved) std::fprintf(stderr, " %lld", (long long)id);
+    std::fprintf(stderr, "; dispatches saved %zu -> %zu\n", before, best);
+  }
+  relocation = allocateBuffer(device, total);
+  ++allocations;
+  plan = movedTo(moved, relocation->address(), &offset);
+  for (const auto &[id, at] : offset) resources[size_t(id)] = relocation->address() + at;
 }
 
 double Invocation::timeNode(size_t index, uint64_t iterations) {

@@ -115,7 +115,10 @@ struct Chain {
   // member's block, offset of its PartialSource in the chain block}.
   std::vector<std::array<size_t, 3>> deferrable;
 };
-std::vector<Chain> findChains(const Plan &plan, const std::vector<bool> &temporary);
+// `refused` (optional) receives the members of every chain refused only because its buffers
+// overlap in a way row-by-row execution would change.
+std::vector<Chain> findChains(const Plan &plan, const std::vector<bool> &temporary,
+                              std::vector<std::vector<size_t>> *refused = nullptr);
 // Split linears whose every reader is a deferrable chain operand leave their combine to those
 // chains: returns the patched linear launches (by plan index) and fills the chains' sources.
 std::map<size_t, Launch> deferCombines(const Plan &plan, const std::vector<bool> &temporary, std::vector<Chain> &chains);
@@ -207,8 +210,12 @@ struct Invocation {
   // graphs and any graph whose units change are dropped and rebuilt at their next use.
   void rebind(const std::vector<Argument> &arguments);
   uint64_t graphInstantiations();
-  // {planned heap bytes, library workspace bytes, device allocations made by the bind}.
+  // {heap bytes, other device memory the binding owns (private workspaces, moved temporaries),
+  // device allocations made by the binding}.
   std::array<uint64_t, 3> memory() const;
+  // Temporaries the inferred graph moved out of storage the plan shares (relocateForChains).
+  std::shared_ptr<Buffer> relocation;
+  bool relocationDecided = false;
   size_t nodeCount() const { return plan.nodes.size(); }
   size_t graphNodeCount(int mode, uint64_t batch);
   size_t graphEdgeCount(int mode, uint64_t batch);
@@ -233,6 +240,7 @@ private:
   friend std::array<double, 2> runConcurrently(const std::vector<Invocation *> &, int, uint64_t, uint64_t, bool);
   void validate(int mode, uint64_t batch) const;
   void requireCurrent() const;                      // refuses a superseded static binding
+  void relocateForChains();
   GraphExec &inferredUnits();
   double timeLaunch(const Launch &launch, uint64_t iterations);
   GraphExec &graphFor(int mode, uint64_t batch);
@@ -257,6 +265,9 @@ struct ProgramState {
   void *entryContext = nullptr;                     // native entries: the compiled plan
   std::vector<uint64_t> bufferBytes;
   std::vector<std::string> scalarTypes;
+  // Bytes of each plan resource by host-entry resource id (temporaries; 0 where unknown: externals,
+  // entries written by hand). The inferred graph moves a temporary only when its size is known.
+  std::vector<uint64_t> resourceBytes;
   std::shared_ptr<ProgramState> aliasFallback;
   std::shared_ptr<void> owner;                      // keeps compiled state alive
 };

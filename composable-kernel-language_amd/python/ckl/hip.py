@@ -344,8 +344,9 @@ class Invocation(_Closable):
         return self._memory()[0]
 
     @property
-    def workspace_bytes(self) -> int:
-        """Bytes of device workspace the binding gave its library kernels."""
+    def private_bytes(self) -> int:
+        """Device memory the binding owns besides its heaps: private workspaces (ckl_workspace) and
+        temporaries the inferred graph moved out of storage the plan shares."""
         return self._memory()[1]
 
     @property

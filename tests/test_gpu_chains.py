@@ -69,12 +69,14 @@ def test_chained_graph_is_bit_identical_to_ordinary(device, config):
     reference = oracle.expected(initial, c, c.steps)
     for reuse, inv in session.invocations.items():
         launches = inv.launch_count(mode="graph", batch_size=1)
+        # With storage reuse the executor moves a chain output that the plan placed in a chain
+        # input's storage to memory of its own, so the same chains are taken; what it moves is
+        # at most the temporaries' storage without reuse.
+        assert launches == chained_launches(c), reuse
         if reuse:
-            # Storage reuse may alias a fused linear's x with a differently sized row it writes;
-            # such a chain runs unfused (the executor's overlap check).
-            assert chained_launches(c) <= launches <= 1 + 8 * c.layers + 2
+            assert inv.private_bytes <= session.invocations[False].heap_bytes
         else:
-            assert launches == chained_launches(c)
+            assert inv.private_bytes == 0
         if c.batch > 16:
             # q/k/v and gate/up multiply one x each: shared-operand launches of the MFMA path.
             names = [name for name, _ in inv.units()]
