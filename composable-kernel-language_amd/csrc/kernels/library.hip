@@ -930,19 +930,39 @@ CKL_LINEAR_SHARED(4, 3)
 __device__ __forceinline__ float2 rotate(float2 s, float2 cs) {
   return make_float2(__builtin_fmaf(s.x, cs.x, -(s.y * cs.y)), __builtin_fmaf(s.x, cs.y, s.y * cs.x));
 }
+// Two adjacent pairs (elements c .. c+3) and their two (cos, sin) entries, each one 128-bit access;
+// each pair rounds exactly as `rotate` alone.
+__device__ __forceinline__ float4 rotate2(float4 s, float4 cs) {
+  const float2 lo = rotate(make_float2(s.x, s.y), make_float2(cs.x, cs.y));
+  const float2 hi = rotate(make_float2(s.z, s.w), make_float2(cs.z, cs.w));
+  return make_float4(lo.x, lo.y, hi.x, hi.y);
+}
+// Pairs a rope worker rotates: two when R is even (python/ckl/library.py sizes the grid alike),
+// so its q, k and table accesses are 128 bits wide; one when R is odd.
+__device__ __forceinline__ int rope_unit(int R) { return (R & 1) ? 1 : 2; }
+__device__ __forceinline__ bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+// A source read 4 floats at a time at 16-byte-aligned element offsets stays aligned.
+__device__ __forceinline__ bool aligned16(const PartialSource &src, const float *own) {
+  return src.parts ? aligned16(src.partials) && (src.planeStride & 3) == 0 : aligned16(own);
+}
 __device__ void rope_body(const RopeArgs &a, int block) {
+  const int unit = rope_unit(a.R), per = a.R / unit;
   long i = long(block) * kBlock + threadIdx.x;
-  long pairs = long(a.B) * a.A * a.R;
-  if (i >= pairs) return;
+  if (i >= long(a.B) * a.A * per) return;
   int p = load_position(a.position);
   if (p < 0 || p >= a.T) return;
-  int r = int(i % a.R);
-  long bh = i / a.R;
-  int h = int(bh % a.A), b = int(bh / a.A);
-  long c = long(b) * (2L * a.R * a.A) + long(h) * (2 * a.R) + 2 * r;
-  float2 s = *reinterpret_cast<const float2 *>(a.src + c);
-  float2 cs = *reinterpret_cast<const float2 *>(a.table + (long(p) * a.R + r) * 2);
-  *reinterpret_cast<float2 *>(a.dst + c) = rotate(s, cs);
+  const int r = int(i % per) * unit;
+  const long bh = i / per;
+  const long c = bh * (2L * a.R) + 2 * r;               // = b*(2R*A) + h*2R + 2r
+  const float *table = a.table + (long(p) * a.R + r) * 2;
+  if (unit == 2 && aligned16(a.src) && aligned16(a.dst) && aligned16(a.table)) {
+    *reinterpret_cast<float4 *>(a.dst + c) =
+        rotate2(*reinterpret_cast<const float4 *>(a.src + c), *reinterpret_cast<const float4 *>(table));
+    return;
+  }
+  for (int j = 0; j < unit; ++j)
+    *reinterpret_cast<float2 *>(a.dst + c + 2 * j) =
+        rotate(*reinterpret_cast<const float2 *>(a.src + c + 2 * j), *reinterpret_cast<const float2 *>(table + 2 * j));
 }
 CKL_ENTRY(rope, RopeArgs, rope_body)
 
@@ -972,29 +992,45 @@ __device__ void append_kv_body(const AppendArgs &a, int block) {
 }
 CKL_ENTRY(append_kv, AppendArgs, append_kv_body)
 
-// rope(q), rope(k) -> append_kv as one launch of rope's geometry: thread (b, h, r) rotates the
-// pair (2r, 2r+1) of q and of k, writes q's (and k's, unless only append reads it), and appends
-// the rotated k pair and v's pair to the caches at the current position. (D = 2R, so element
-// h*D + 2r of k and v is the same index c as the rotated pair.)
+// rope(q), rope(k) -> append_kv as one launch of rope's geometry: a worker rotates rope_unit(R)
+// adjacent pairs of q and of k (128-bit accesses when R is even and the buffers allow), writes q's
+// (and k's, unless only append reads it), and appends the rotated k and v's elements to the caches
+// at the current position. (D = 2R, so element h*D + 2r of k and v is the same index c as the
+// rotated pair.)
+__device__ __forceinline__ void rope_append_pair(const RopeAppendChainArgs &a, long c, long row, const float *table) {
+  const float2 cs = *reinterpret_cast<const float2 *>(table);
+  *reinterpret_cast<float2 *>(a.q.dst + c) = rotate(source2(a.qsrc, a.q.src, c), cs);
+  const float2 kr = rotate(source2(a.ksrc, a.k.src, c), cs);
+  if (a.k.dst) *reinterpret_cast<float2 *>(a.k.dst + c) = kr;
+  *reinterpret_cast<float2 *>(a.append.kc + row) = kr;
+  *reinterpret_cast<float2 *>(a.append.vc + row) = source2(a.v, a.append.v, c);
+}
 __device__ void rope__rope__append_kv_body(const RopeAppendChainArgs &a, int block) {
   const RopeArgs &q = a.q, &k = a.k;
   const AppendArgs &ap = a.append;
+  const int unit = rope_unit(q.R), per = q.R / unit;
   long i = long(block) * kBlock + threadIdx.x;
-  long pairs = long(q.B) * q.A * q.R;
-  if (i >= pairs) return;
+  if (i >= long(q.B) * q.A * per) return;
   int p = load_position(q.position);
   if (p < 0 || p >= q.T) return;
-  int r = int(i % q.R);
-  long bh = i / q.R;
-  int h = int(bh % q.A), b = int(bh / q.A);
-  long c = long(b) * (2L * q.R * q.A) + long(h) * (2 * q.R) + 2 * r;
-  float2 cs = *reinterpret_cast<const float2 *>(q.table + (long(p) * q.R + r) * 2);
-  *reinterpret_cast<float2 *>(q.dst + c) = rotate(source2(a.qsrc, q.src, c), cs);
-  float2 kr = rotate(source2(a.ksrc, k.src, c), cs);
-  if (k.dst) *reinterpret_cast<float2 *>(k.dst + c) = kr;
-  long row = (((long(ap.layer) * ap.B * ap.A) + bh) * ap.T + p) * ap.D + 2 * r;
-  *reinterpret_cast<float2 *>(ap.kc + row) = kr;
-  *reinterpret_cast<float2 *>(ap.vc + row) = source2(a.v, ap.v, c);
+  const int r = int(i % per) * unit;
+  const long bh = i / per;
+  const long c = bh * (2L * q.R) + 2 * r;
+  const long row = (((long(ap.layer) * ap.B * ap.A) + bh) * ap.T + p) * ap.D + 2 * r;
+  const float *table = q.table + (long(p) * q.R + r) * 2;
+  const bool wide = unit == 2 && aligned16(a.qsrc, q.src) && aligned16(a.ksrc, k.src) && aligned16(a.v, ap.v) &&
+                    aligned16(q.dst) && (!k.dst || aligned16(k.dst)) && aligned16(q.table) && aligned16(ap.kc) &&
+                    aligned16(ap.vc);
+  if (!wide) {
+    for (int j = 0; j < unit; ++j) rope_append_pair(a, c + 2 * j, row + 2 * j, table + 2 * j);
+    return;
+  }
+  const float4 cs = *reinterpret_cast<const float4 *>(table);
+  *reinterpret_cast<float4 *>(q.dst + c) = rotate2(source4(a.qsrc, q.src, c), cs);
+  const float4 kr = rotate2(source4(a.ksrc, k.src, c), cs);
+  if (k.dst) *reinterpret_cast<float4 *>(k.dst + c) = kr;
+  *reinterpret_cast<float4 *>(ap.kc + row) = kr;
+  *reinterpret_cast<float4 *>(ap.vc + row) = source4(a.v, ap.v, c);
 }
 CKL_ENTRY(rope__rope__append_kv, RopeAppendChainArgs, rope__rope__append_kv_body)
 
@@ -1453,18 +1489,24 @@ __device__ void rope_attention_rows(const RopeAttentionChainArgs &a, int block) 
     load_key_batch<NT, P>(first, sc.kc + (long(sc.layer) * sc.B * sc.A + bh) * long(sc.T) * sc.D, sc.D, layout,
                           firstBase, p);
   if (inRange) {
+    // One pair a thread, 64-bit accesses: this rotation runs while every wave holds its first batch
+    // of key rows in registers, and the 128-bit form (two pairs a thread, 4-wide partial-plane sums)
+    // raised the kernel from 69 to 196 VGPRs with scratch, occupancy 7 -> 2. The rotation and append
+    // take ~2 us of the ~85 us launch (large decoder), and the standalone rope and rope -> append_kv
+    // kernels use 128-bit accesses.
+    const long row0 = (((long(ap.layer) * ap.B * ap.A) + bh) * ap.T + p) * ap.D;
+    const float *table = q.table + long(p) * q.R * 2;
     for (int r = threadIdx.x; r < q.R; r += blockDim.x) {
-      long c = bh * (2L * q.R) + 2 * r;              // = b*(2R*A) + h*2R + 2r
-      float2 cs = *reinterpret_cast<const float2 *>(q.table + (long(p) * q.R + r) * 2);
-      float2 qr = rotate(source2(a.qsrc, q.src, c), cs);
+      const long c = bh * (2L * q.R) + 2 * r;        // = b*(2R*A) + h*2R + 2r
+      const float2 cs = *reinterpret_cast<const float2 *>(table + 2 * r);
+      const float2 qr = rotate(source2(a.qsrc, q.src, c), cs);
       *reinterpret_cast<float2 *>(q.dst + c) = qr;
       *reinterpret_cast<float2 *>(qrow + 2 * r) = qr;
-      float2 kr = rotate(source2(a.ksrc, k.src, c), cs);
+      const float2 kr = rotate(source2(a.ksrc, k.src, c), cs);
       if (k.dst) *reinterpret_cast<float2 *>(k.dst + c) = kr;
       *reinterpret_cast<float2 *>(krow + 2 * r) = kr;
-      long row = (((long(ap.layer) * ap.B * ap.A) + bh) * ap.T + p) * ap.D + 2 * r;
-      *reinterpret_cast<float2 *>(ap.kc + row) = kr;
-      *reinterpret_cast<float2 *>(ap.vc + row) = source2(a.v, ap.v, c);
+      *reinterpret_cast<float2 *>(ap.kc + row0 + 2 * r) = kr;
+      *reinterpret_cast<float2 *>(ap.vc + row0 + 2 * r) = source2(a.v, ap.v, c);
     }
     // The sequential dot product reads the appended key row from the cache after the barrier.
     if (!vector) __builtin_amdgcn_s_waitcnt(kWaitStores);

@@ -272,16 +272,19 @@ const char *ropeAppendChain(const Members &m, const Internal &internal, Launch &
   if (ap.k != k.dst || ap.B != q.B || ap.A != q.A || ap.D != 2 * q.R || ap.T != q.T || ap.layer < 0 || ap.L <= ap.layer)
     return "append_kv does not take the rotated k";
   if (q.B <= 0 || q.A <= 0 || q.R <= 0 || q.T <= 0) return "empty rope";
-  uint64_t pairs = uint64_t(q.B) * uint64_t(q.A) * uint64_t(q.R);
+  // A worker rotates two adjacent pairs when R is even (rope_unit in the kernel library).
+  const uint64_t unit = (q.R & 1) ? 1 : 2;
+  uint64_t workers = uint64_t(q.B) * uint64_t(q.A) * uint64_t(q.R) / unit, bytes = 8 * unit;
   uint64_t cache = uint64_t(ap.B) * uint64_t(ap.A) * uint64_t(ap.T) * uint64_t(ap.D);
   if (internal(1, k.dst)) c.k.dst = nullptr;
-  std::vector<Range> ranges{rows(q.src, pairs, 8, false), rows(q.dst, pairs, 8, true), rows(k.src, pairs, 8, false),
-                            rows(ap.v, pairs, 8, false), whole(q.table, 8ull * uint64_t(q.T) * uint64_t(q.R)),
-                            whole(q.position, 4), slab(ap.kc + int64_t(ap.layer) * int64_t(cache), 4 * cache, true),
+  std::vector<Range> ranges{rows(q.src, workers, bytes, false), rows(q.dst, workers, bytes, true),
+                            rows(k.src, workers, bytes, false), rows(ap.v, workers, bytes, false),
+                            whole(q.table, 8ull * uint64_t(q.T) * uint64_t(q.R)), whole(q.position, 4),
+                            slab(ap.kc + int64_t(ap.layer) * int64_t(cache), 4 * cache, true),
                             slab(ap.vc + int64_t(ap.layer) * int64_t(cache), 4 * cache, true)};
-  if (c.k.dst) ranges.push_back(rows(k.dst, pairs, 8, true));
+  if (c.k.dst) ranges.push_back(rows(k.dst, workers, bytes, true));
   if (!hazardFree(ranges)) return kOverlap;
-  out.grid[0] = cdiv(pairs, 256);
+  out.grid[0] = cdiv(workers, 256);
   out.block[0] = 256;
   out.shared = 0;
   setArguments(out, c);

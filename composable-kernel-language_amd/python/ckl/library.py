@@ -188,7 +188,8 @@ def _rope(shapes, consts, ext):
     a = c // (2 * r)
     if not (ext[0] >= r and ext[1:] == (a, b)):
         return None
-    return Launch(_cdiv(b * a * r, BLOCK), (b, a, r, t))
+    unit = 1 if r % 2 else 2      # rope_unit: pairs a thread rotates (two: 128-bit accesses)
+    return Launch(_cdiv(b * a * (r // unit), BLOCK), (b, a, r, t))
 
 
 def _append_kv(shapes, consts, ext):
