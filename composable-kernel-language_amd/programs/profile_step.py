@@ -1,6 +1,7 @@
 """Run decode steps of one decoder configuration for a kernel profiler.
 
-Binds the decode program (storage reuse on) to seeded synthetic state, sets the position to the
+Binds the decode program (storage reuse off: the plan of bench.py's headline "inferred" variant)
+to seeded synthetic state, sets the position to the
 configuration's prefill position (so attention covers context rows, as in the timed steps; the
 cache contents do not change kernel durations) and executes `--steps` inferred steps in mode
 "stream": the inferred graph's contracted launches issued on the stream, so a profiler sees every
