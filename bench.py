@@ -11,7 +11,9 @@ generation with HIP events on the invocation stream; samples rotate and reverse 
 order; the median microseconds per decode step is reported. Every run is verified
 (run.py:172-196): each variant's first generation in full (tokens, history, position, logits,
 the cache rows written, the prefill rows and unused suffix unchanged, sentinel tails), every
-warmup and timed sample's tokens, history, position and logits, and the weights after all.
+warmup and timed sample's tokens, history, position and logits, and the weights after all. A timed
+sample's state is downloaded right after it and checked once all samples have run, so that no
+check leaves the GPU idle between samples (after ~30 ms idle a large step runs ~2% slower).
 
 Variants (run.py:24-38 plus ablations):
   sequential / capture / inferred       ordinary launches, single-stream capture, inferred graph
@@ -146,11 +148,13 @@ def time_variants(session, c, steps, warmup, expected, log_prefix, only=None):
     timed = {name: 0 for name, *_ in rows}
     setup, errors, checked = {}, {name: {} for name, *_ in rows}, {name: 0 for name, *_ in rows}
 
-    def verify(name, count, full=False):
-        found = state.verify_generation(expected[count], full=full, longest=c.steps)
+    def record(name, found):
         for key, value in found.items():
             errors[name][key] = max(errors[name].get(key, 0.0), value)
         checked[name] += 1
+
+    def verify(name, count, full=False):
+        record(name, state.verify_generation(expected[count], full=full, longest=c.steps))
 
     for name, reuse, mode, group in rows:
         inv = session.invocations[reuse]
@@ -162,6 +166,10 @@ def time_variants(session, c, steps, warmup, expected, log_prefix, only=None):
             k = submissions(count, group)
             inv.benchmark(iterations=k, mode=mode, batch_size=group)
             verify(name, k * group)
+    # Timed samples run back to back: each one's final state is downloaded right after it and
+    # checked once all samples have run, so the GPU is not left idle for the tens of milliseconds
+    # a check takes (an idle GPU starts the next sample below its steady-state clocks).
+    captured = []
     for sample, count in enumerate(generations(steps)):
         offset = sample % len(rows)
         order = rows[offset:] + rows[:offset]
@@ -175,7 +183,9 @@ def time_variants(session, c, steps, warmup, expected, log_prefix, only=None):
             metrics[name].append(timing["stream_us"])
             walls[name].append(timing["wall_us"])
             timed[name] += k * group
-            verify(name, k * group)
+            captured.append((name, k * group, state.capture()))
+    for name, count, capture in captured:
+        record(name, state.check_capture(capture, expected[count]))
     state.verify_read_only()
     table = {}
     for name, reuse, mode, group in rows:

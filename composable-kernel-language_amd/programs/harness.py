@@ -167,9 +167,22 @@ class DecoderState:
         row past the longest generation (`longest` steps) unchanged, and the caches' tails.
         `expected` holds tokens, history, position, logits and the written cache rows
         (kc_rows, vc_rows: [L, B, A, steps, D]). Returns the largest errors."""
+        out = self.check_capture(self.capture(), expected)
+        if not full:
+            return out
+        return {**out, **self._verify_caches(expected, longest)}
+
+    def capture(self) -> dict:
+        """Download what every generation is checked on (tokens, history, position, logits, with
+        their sentinel tails), so that the check can run later (check_capture)."""
+        return {name: self.download(name, with_tail=True) for name in ("tokens", "history", "position", "logits")}
+
+    def check_capture(self, captured: dict, expected: dict) -> dict:
+        """The checks of verify_generation without `full` on a capture() taken after the
+        generation. Returns the largest logits errors."""
         out = {}
         for name in ("tokens", "history", "position", "logits"):
-            actual = self.download(name, with_tail=True)
+            actual = captured[name]
             size = self.initial[name].size
             if not np.all(actual[size:] == SENTINEL):
                 raise AssertionError(f"{name}: tail overwritten")
@@ -184,8 +197,10 @@ class DecoderState:
             out["logits_normwise"] = normwise_error(actual, expected[name])
             if out["logits_normwise"] > LOGITS_NORMWISE:
                 raise AssertionError(f"logits: row-normwise error {out['logits_normwise']:.3e} > {LOGITS_NORMWISE}")
-        if not full:
-            return out
+        return out
+
+    def _verify_caches(self, expected: dict, longest: int) -> dict:
+        out = {}
         start, steps = int(self.initial["position"][0]), int(expected["steps"])
         for name in ("kc", "vc"):
             actual = self.download(name, with_tail=True)
