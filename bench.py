@@ -38,7 +38,8 @@ every burst's state is checked against the requests run one after another.
 
 Output: one short JSON line on stdout (headline, roofline, CPU baseline, one summary per other
 configuration); the full result (every variant's samples, kernel families, setup costs, vector
-pipeline, independent requests) goes to --output (default gpurun_out/bench_detail.json); progress
+pipeline, independent requests) goes to --output (default: ckl_bench_detail.json in the system's
+temporary directory); progress
 on stderr. The headline `value` is the large decoder's inferred-graph median µs/step (the largest
 single-GPU configuration of BASELINE.json). The CPU baseline times the same NumPy decoder step in
 two child processes started before any GPU call (all cores, then one thread) after the GPU timing.
@@ -68,7 +69,7 @@ HBM_PEAK = 8.0e12          # MI355X HBM3E bytes/s
 METRIC = "median µs/decode step: inferred hipGraph vs stream capture; scratch bytes"
 HEADLINE = "large"
 GENERATION = 16            # greedy steps per generation
-DEFAULT_DETAIL = ROOT / "gpurun_out" / "bench_detail.json"
+DEFAULT_DETAIL = Path(tempfile.gettempdir()) / "ckl_bench_detail.json"
 
 
 def log(*parts):
