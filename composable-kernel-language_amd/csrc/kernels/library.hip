@@ -1464,6 +1464,30 @@ CKL_ENTRY_ATTR(attention_scores__softmax__attention_values_nt, AttentionChainArg
 // [0, T) only if the caller lets it run past the cache capacity; then rope and append write
 // nothing and the attention reads q's buffer, as the separate dispatches would.
 // Dynamic LDS: the row of T scores (padded to 4 floats), then the D-float query and key rows.
+// Planes of a rotation operand requested up front (rope_attention_rows): a pair from each of the
+// first kRopeRequest planes (a source of fewer planes re-reads its last one) or, without planes,
+// the pair itself; sum_pair adds them as source2 does.
+constexpr int kRopeRequest = 4;
+__device__ __forceinline__ void request_pair(const PartialSource &src, const float *own, long i,
+                                             float2 (&out)[kRopeRequest]) {
+  if (src.parts == 0) {
+    out[0] = *reinterpret_cast<const float2 *>(own + i);
+    return;
+  }
+#pragma unroll
+  for (int j = 0; j < kRopeRequest; ++j)
+    out[j] = *reinterpret_cast<const float2 *>(src.partials + long(min(j, src.parts - 1)) * src.planeStride + i);
+}
+__device__ __forceinline__ float2 sum_pair(const PartialSource &src, const float2 (&in)[kRopeRequest]) {
+  if (src.parts == 0) return in[0];
+  float2 t = make_float2(0.f, 0.f);
+#pragma unroll
+  for (int j = 0; j < kRopeRequest; ++j) {
+    t.x += j < src.parts ? in[j].x : 0.f;
+    t.y += j < src.parts ? in[j].y : 0.f;
+  }
+  return t;
+}
 template <bool NT, int P>
 __device__ void rope_attention_rows(const RopeAttentionChainArgs &a, int block) {
   extern __shared__ float rowScores[];
@@ -1484,11 +1508,39 @@ __device__ void rope_attention_rows(const RopeAttentionChainArgs &a, int block) 
   const KeyLayout<P> layout(vector ? sc.D : 4 * P);
   const int firstBase = wave * layout.rowsPerBatch();
   const bool early = vector && inRange && p >= 1;
+  // With one pair a thread and at most kRopeRequest planes a source, a thread's rotation operands
+  // (its q, k and v pairs' planes and the (cos, sin) entry) are requested before the first key
+  // batch, so that they are not queued behind the key rows every workgroup requests at once, and
+  // added after the batch has been issued (in plane order, as source2 adds them).
+  const bool requestFirst = inRange && q.R <= int(blockDim.x) && a.qsrc.parts <= kRopeRequest &&
+                            a.ksrc.parts <= kRopeRequest && a.v.parts <= kRopeRequest;
+  const int pair = threadIdx.x;
+  const long pairIndex = bh * (2L * q.R) + 2 * pair;          // = b*(2R*A) + h*2R + 2r
+  float2 qPlanes[kRopeRequest], kPlanes[kRopeRequest], vPlanes[kRopeRequest], pairTable = make_float2(0.f, 0.f);
+  if (requestFirst && pair < q.R) {
+    pairTable = *reinterpret_cast<const float2 *>(q.table + long(p) * q.R * 2 + 2 * pair);
+    request_pair(a.qsrc, q.src, pairIndex, qPlanes);
+    request_pair(a.ksrc, k.src, pairIndex, kPlanes);
+    request_pair(a.v, ap.v, pairIndex, vPlanes);
+  }
   KeyBatch first;
   if (early)
     load_key_batch<NT, P>(first, sc.kc + (long(sc.layer) * sc.B * sc.A + bh) * long(sc.T) * sc.D, sc.D, layout,
                           firstBase, p);
-  if (inRange) {
+  if (requestFirst) {
+    if (pair < q.R) {
+      const long row0 = (((long(ap.layer) * ap.B * ap.A) + bh) * ap.T + p) * ap.D;
+      const float2 qr = rotate(sum_pair(a.qsrc, qPlanes), pairTable);
+      *reinterpret_cast<float2 *>(q.dst + pairIndex) = qr;
+      *reinterpret_cast<float2 *>(qrow + 2 * pair) = qr;
+      const float2 kr = rotate(sum_pair(a.ksrc, kPlanes), pairTable);
+      if (k.dst) *reinterpret_cast<float2 *>(k.dst + pairIndex) = kr;
+      *reinterpret_cast<float2 *>(krow + 2 * pair) = kr;
+      *reinterpret_cast<float2 *>(ap.kc + row0 + 2 * pair) = kr;
+      *reinterpret_cast<float2 *>(ap.vc + row0 + 2 * pair) = sum_pair(a.v, vPlanes);
+    }
+    if (!vector) __builtin_amdgcn_s_waitcnt(kWaitStores);
+  } else if (inRange) {
     // One pair a thread, 64-bit accesses: this rotation runs while every wave holds its first batch
     // of key rows in registers, and the 128-bit form (two pairs a thread, 4-wide partial-plane sums)
     // raised the kernel from 69 to 196 VGPRs with scratch, occupancy 7 -> 2. The rotation and append
